@@ -1,0 +1,291 @@
+"""Benchmark: synthetic 40-layer MoE-FFN stack on one MI355X.
+
+One step = one request of the headline workload: a 4096-token prefill in two
+2048-token chunks (W8A16 grouped MFMA GEMMs) followed by 33 serial decode
+tokens (W8A8 expert GEMVs, the 40-layer decode step replayed as a HIP graph),
+over random-init int8 group-128 weights (~33.4 GB) resident in HBM.
+
+Prints one JSON line.  value = prefill tok/s; decode tok/s, decode HBM GB/s
+and the roofline of the dominant kernel ride along.  Per-phase kernel times
+come from HIP events recorded on the launch stream inside the timed steps.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+PREFILL_TOKENS, CHUNK, DECODE_TOKENS = 4096, 2048, 33
+H, I, E, K = 2048, 512, 256, 8
+GU_EXPERT_BYTES = 2 * I * H + 2 * I * (H // 128) * 4        # 2,162,688
+DN_EXPERT_BYTES = H * I + H * (I // 128) * 4                # 1,081,344
+EXPERT_BYTES = GU_EXPERT_BYTES + DN_EXPERT_BYTES            # 3,244,032
+DECODE_LAYER_BYTES = 9 * EXPERT_BYTES + E * H * 2 + H * 2   # 30,248,960
+PREFILL_PHASES = ['norm_gate', 'router_logits', 'topk', 'route_plan', 'gate_up', 'down',
+                  'combine']
+DECODE_PHASES = ['decode_router', 'decode_gate_up', 'decode_down']
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument('--gpus', type=int, default=1)
+    p.add_argument('--steps', type=int, default=3)
+    p.add_argument('--warmup', type=int, default=1)
+    p.add_argument('--layers', type=int, default=40)
+    p.add_argument('--no-cpu-baseline', action='store_true')
+    p.add_argument('--no-events', action='store_true',
+                   help='time whole steps only (no per-phase HIP events)')
+    return p.parse_args()
+
+
+def log(msg):
+    print(f'[bench] {msg}', file=sys.stderr, flush=True)
+
+
+def make_events(n):
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    for e in evs:
+        e.record()  # creates the underlying hipEvent
+    return evs
+
+
+def prefill_bytes(active, tokens=CHUNK):
+    routes = tokens * K
+    return {
+        'gate_up': (active + 1) * GU_EXPERT_BYTES + tokens * H * 2 + (routes + tokens) * I * 2,
+        'down': (active + 1) * DN_EXPERT_BYTES + (routes + tokens) * I * 2
+        + (routes + tokens) * H * 2,
+    }
+
+
+def prefill_flops(tokens=CHUNK):
+    rows = tokens * K + tokens
+    return {'gate_up': 2.0 * rows * 2 * I * H, 'down': 2.0 * rows * H * I}
+
+
+def cpu_baseline(stack, x, dec_in, cores):
+    """The CPU oracle (dequantize-then-matmul, the reference arithmetic on the
+    host) on a bounded sample: one 2048-token prefill chunk through one layer
+    and one decode token through every layer; extrapolated to tok/s."""
+    from oracle import moe_oracle as O
+    from localmoe35ba3b_amd.runtime.stack import EPS
+    torch.set_num_threads(cores)
+    layer0 = stack.layer_host(0)
+    h = x[:CHUNK].float().cpu().numpy()
+    t0 = time.perf_counter()
+    O.moe_layer(h, layer0, k=K, eps=EPS)
+    t_chunk_layer = time.perf_counter() - t0
+    log(f'cpu prefill sample: {t_chunk_layer:.2f} s')
+    del layer0
+    # decode: the experts a token selects per layer (host copies made first)
+    hd = dec_in[0].float().cpu().numpy()
+    hosts, t_dec = [], 0.0
+    ids_buf = torch.empty((1, K), dtype=torch.int32, device=x.device)
+    hg = dec_in[0].clone()
+    for l in range(stack.L):
+        stack.layer_forward(hg, l, ids_buf)
+        hosts.append(stack.layer_host(l, experts=ids_buf.cpu().numpy()[0]))
+    for l in range(stack.L):
+        t0 = time.perf_counter()
+        hd, _ = O.moe_layer(hd, hosts[l], k=K, eps=EPS)
+        t_dec += time.perf_counter() - t0
+    prefill_tok_s = CHUNK / (t_chunk_layer * stack.L)
+    return {
+        'value': round(prefill_tok_s, 3), 'unit': 'tok/s', 'cores': cores, 'kind': 'port',
+        'decode_tok_s': round(1.0 / t_dec, 4),
+        'sample': (f'oracle (torch-CPU dequant + F.linear, numpy W8A8) on {cores} threads: one '
+                   f'2048-token prefill chunk through 1 of {stack.L} layers '
+                   f'({t_chunk_layer:.2f} s, prefill extrapolated x{stack.L}) and one decode '
+                   f'token through all {stack.L} layers ({t_dec:.2f} s)'),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f'bench.py measures one GPU; --gpus {args.gpus} is not supported by this build '
+              '(the path would shard experts across GPUs, see DESIGN.md)', file=sys.stderr)
+        sys.exit(2)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from localmoe35ba3b_amd.runtime.stack import SyntheticMoEStack
+
+    dev = torch.device('cuda:0')
+    t_build = time.perf_counter()
+    stack = SyntheticMoEStack(layers=args.layers, seed=4, device=dev, max_tokens=CHUNK)
+    torch.cuda.synchronize()
+    t_build = time.perf_counter() - t_build
+    log(f'stack built: {stack.L} layers, {stack.bank_bytes() / 1e9:.2f} GB in HBM, {t_build:.1f} s')
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    x = torch.randn((PREFILL_TOKENS, H), generator=gen, device=dev).to(torch.bfloat16)
+    dec_in = torch.randn((DECODE_TOKENS, 1, H), generator=gen, device=dev).to(torch.bfloat16)
+    nchunks = PREFILL_TOKENS // CHUNK
+    L = stack.L
+
+    # decode step = all layers on one token, captured once as a HIP graph
+    static = dec_in[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        stack.forward(static.clone())
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        stack.forward(static)
+
+    pf_events = None if args.no_events else [[make_events(8) for _ in range(L)]
+                                             for _ in range(nchunks)]
+
+    def prefill(events=None):
+        out = x.clone()
+        for c in range(nchunks):
+            hc = out[c * CHUNK:(c + 1) * CHUNK]
+            for l in range(L):
+                stack.layer_forward(hc, l, events=None if events is None else events[c][l])
+        return out
+
+    def decode():
+        for i in range(DECODE_TOKENS):
+            static.copy_(dec_in[i])
+            graph.replay()
+
+    for _ in range(args.warmup):
+        prefill()
+        decode()
+    torch.cuda.synchronize()
+    log('warmup done')
+
+    marks = [make_events(3) for _ in range(args.steps)]
+    phase_ms = {p: 0.0 for p in PREFILL_PHASES}
+    t_prefill = t_decode = 0.0
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    for s in range(args.steps):
+        m = marks[s]
+        m[0].record()
+        prefill(pf_events)
+        m[1].record()
+        decode()
+        m[2].record()
+        if pf_events is not None:
+            torch.cuda.synchronize()
+            for c in range(nchunks):
+                for l in range(L):
+                    ev = pf_events[c][l]
+                    for i, p in enumerate(PREFILL_PHASES):
+                        phase_ms[p] += ev[i].elapsed_time(ev[i + 1])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    for m in marks:
+        t_prefill += m[0].elapsed_time(m[1]) / 1e3
+        t_decode += m[1].elapsed_time(m[2]) / 1e3
+    steps = args.steps
+    log(f'timed {steps} steps: {wall:.3f} s')
+    prefill_tok_s = steps * PREFILL_TOKENS / t_prefill
+    decode_tok_s = steps * DECODE_TOKENS / t_decode
+    decode_gbs = DECODE_LAYER_BYTES * L * decode_tok_s / 1e9
+
+    # untimed: routing statistics (active experts per layer-chunk) and the
+    # per-kernel decode times of one eager (non-graph) request
+    ids = torch.empty((CHUNK, K), dtype=torch.int32, device=dev)
+    active = []
+    out = x.clone()
+    for c in range(nchunks):
+        hc = out[c * CHUNK:(c + 1) * CHUNK]
+        for l in range(L):
+            stack.layer_forward(hc, l, ids)
+            active.append(int(torch.unique(ids).numel()))
+    dec_ev = [make_events(4) for _ in range(L)]
+    dec_ms = {p: 0.0 for p in DECODE_PHASES}
+    hd = static.clone()
+    for i in range(DECODE_TOKENS):
+        hd.copy_(dec_in[i])
+        for l in range(L):
+            stack.layer_forward(hd, l, events=dec_ev[l])
+        torch.cuda.synchronize()
+        for l in range(L):
+            for j, p in enumerate(DECODE_PHASES):
+                dec_ms[p] += dec_ev[l][j].elapsed_time(dec_ev[l][j + 1])
+
+    launches_pf = steps * nchunks * L
+    mean_active = float(np.mean(active))
+    kernels = {}
+    if pf_events is not None:
+        pb = [prefill_bytes(a) for a in active]
+        fl = prefill_flops()
+        for p in ('gate_up', 'down'):
+            avg_us = phase_ms[p] / launches_pf * 1e3
+            avg_bytes = float(np.mean([b[p] for b in pb]))
+            kernels['prefill_' + p] = {
+                'avg_us': round(avg_us, 2), 'launches': launches_pf,
+                'total_ms': round(phase_ms[p], 3), 'bytes_per_launch': int(avg_bytes),
+                'gbs': round(avg_bytes / avg_us / 1e3, 1),
+                'tflops': round(fl[p] / avg_us / 1e6, 1)}
+        for p in ('norm_gate', 'router_logits', 'topk', 'route_plan', 'combine'):
+            kernels['prefill_' + p] = {'avg_us': round(phase_ms[p] / launches_pf * 1e3, 2),
+                                       'total_ms': round(phase_ms[p], 3)}
+    n_dec = DECODE_TOKENS * L
+    dec_bytes = {'decode_router': E * H * 2 + H * 2,
+                 'decode_gate_up': 9 * GU_EXPERT_BYTES,
+                 'decode_down': 9 * DN_EXPERT_BYTES}
+    for p in DECODE_PHASES:
+        avg_us = dec_ms[p] / n_dec * 1e3
+        kernels[p] = {'avg_us': round(avg_us, 2), 'launches': n_dec,
+                      'bytes_per_launch': dec_bytes[p],
+                      'gbs': round(dec_bytes[p] / avg_us / 1e3, 1),
+                      'total_ms_per_request': round(dec_ms[p], 3)}
+
+    # dominant kernel by total time within one request
+    per_req = {}
+    if pf_events is not None:
+        per_req['prefill_gate_up'] = phase_ms['gate_up'] / steps
+        per_req['prefill_down'] = phase_ms['down'] / steps
+        per_req['prefill_router_logits'] = phase_ms['router_logits'] / steps
+    for p in DECODE_PHASES:
+        per_req[p] = dec_ms[p]
+    dom = max(per_req, key=per_req.get)
+    roofline = None
+    if 'bytes_per_launch' in kernels.get(dom, {}):
+        k = kernels[dom]
+        achieved = k['bytes_per_launch'] / k['avg_us'] / 1e3
+        roofline = {'bound': 'hbm', 'kernel': dom, 'achieved': round(achieved, 1),
+                    'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4),
+                    'traffic': None, 'bytes_per_launch': k['bytes_per_launch'],
+                    'avg_us': k['avg_us']}
+
+    log('per-kernel decode timing done')
+    cores = min(16, os.cpu_count() or 1)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(stack, x, dec_in, cores)
+
+    line = {
+        'metric': 'MoE-FFN prefill/decode tok/s (4K chunk); decode HBM GB/s and % of peak',
+        'value': round(prefill_tok_s, 1), 'unit': 'tok/s', 'n_gpus': 1, 'steps': steps,
+        'warmup': args.warmup, 'ms_per_step': round(wall / steps * 1e3, 3),
+        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16',
+        'data': 'synthetic (random-init int8 g128 weights, N(0,1) activations)',
+        'config': {'workload': f'{L}-layer MoE-FFN stack: 4096-token prefill (2x2048 chunks, '
+                               f'W8A16) + 33 decode tokens (W8A8 experts), 256 experts top-8 + '
+                               f'shared, hidden 2048, intermediate 512',
+                   'layers': L, 'prefill_tokens': PREFILL_TOKENS, 'chunk': CHUNK,
+                   'decode_tokens': DECODE_TOKENS, 'bank_gb': round(stack.bank_bytes() / 1e9, 2)},
+        'prefill_tok_s': round(prefill_tok_s, 1),
+        'decode_tok_s': round(decode_tok_s, 1),
+        'decode_hbm_gbs': round(decode_gbs, 1),
+        'decode_hbm_frac': round(decode_gbs / HBM_PEAK_GBS, 4),
+        'decode_dtype': 'int8 (W8A8 experts), bf16 (shared expert, router fp64)',
+        'mean_active_experts': round(mean_active, 1),
+        'roofline': roofline,
+        'kernels': kernels,
+        'cpu_baseline': cpu,
+        'build_s': round(t_build, 1),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()

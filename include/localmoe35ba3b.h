@@ -1,0 +1,244 @@
+/*
+ * localmoe35ba3b.h - C ABI of the MI355X (gfx950) quantized MoE-FFN hot path.
+ *
+ * Every entry point takes raw device pointers, 64-bit sizes and a HIP stream
+ * handle passed as `void *` (a `hipStream_t`; NULL is the legacy default
+ * stream).  Launches are asynchronous and stream-ordered; no entry point
+ * synchronises the device, allocates device memory or frees caller memory.
+ * All validation happens on the host before any launch, so a non-zero status
+ * means nothing was enqueued.
+ *
+ * Status codes map onto the exception types the Python operators raise:
+ *   LM_OK      0  success
+ *   LM_EINVAL  1  ValueError   (bad geometry, dtype, id range, ...)
+ *   LM_ENOMEM  2  MemoryError  (a workspace or capacity bound is exceeded)
+ *   LM_ELAUNCH 3  RuntimeError (the HIP runtime refused a launch)
+ * lm_last_error() returns the message of the last failing call on the
+ * calling host thread.
+ *
+ * Data formats (identical to the reference converter's artifact format):
+ *   weights  q int8 [N, K] row-major (K contiguous), K % 128 == 0
+ *   scales   s fp32 [N, K/128]: w[n, k] ~= q[n, k] * s[n, k/128]
+ *   expert banks are [E, N, K] / [E, N, K/128] with arbitrary expert stride.
+ *   activations are bf16 (LM_BF16) or fp16 (LM_FP16) row-major.
+ *
+ * Reference citations are to heliosz616/LocalMoe35Ba3b (qwen35_deploy/...)
+ * and to the Transformers 5.15.0 Qwen3_5Moe modeling file ("HF").
+ */
+#ifndef LOCALMOE35BA3B_H
+#define LOCALMOE35BA3B_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LM_OK 0
+#define LM_EINVAL 1
+#define LM_ENOMEM 2
+#define LM_ELAUNCH 3
+
+#define LM_BF16 0
+#define LM_FP16 1
+#define LM_FP32 2
+
+/* Library identification and the message of the last error on this thread. */
+const char *lm_version(void);
+const char *lm_last_error(void);
+
+/* Offline weight quantizer: s = max(amax_g|w| / 127, 1e-30) per 128-wide K
+ * group, q = clamp(round_half_even(w / s), -127, 127).  w fp32 [rows, k].
+ * Replaces convert.quantize (convert.py:31-37). */
+int lm_quantize_weight_g128(const float *w, int8_t *q, float *s,
+                            int64_t rows, int64_t k, void *stream);
+
+/* Dynamic activation quantization per row and 128-group:
+ * s = max(amax, 1e-10) * (1/127), q = rint(x / s).  x [rows, k] (x_dtype).
+ * Replaces w8a8.quantize / w8a8._quant (w8a8.py:8-22). */
+int lm_act_quant_g128(const void *x, int x_dtype, int8_t *q, float *s,
+                      int64_t rows, int64_t k, void *stream);
+
+/* Dense W8A16: y[m, n] = sum_k x[m, k] * dtype(q[n, k] * s[n, k/128]),
+ * fp32 accumulation, y in the activation dtype.  m <= 8 runs the HBM
+ * streaming GEMV, larger m the MFMA GEMM.  large_tile only selects the
+ * MFMA tile height.  Replaces int8.linear / int8._linear (int8.py:9-37). */
+int lm_w8a16_linear(const void *x, const int8_t *q, const float *s, void *y,
+                    int64_t m, int64_t n, int64_t k, int dtype, int large_tile,
+                    void *stream);
+
+/* Grouped W8A16 decode GEMV over a device descriptor table
+ * table[e, 5] = {gate_up.q, gate_up.s, down.q, down.s, slot} (int64):
+ * y[e, :] = x[shared ? 0 : e, :] . dequant(table[e, field..field+1])^T.
+ * Replaces int8.grouped_linear / int8._grouped_linear (int8.py:213-237). */
+int lm_w8a16_grouped_gemv(const void *x, const int64_t *table, void *y,
+                          int64_t experts, int64_t n, int64_t k, int field,
+                          int shared, void *stream);
+
+/* Grouped W8A8 decode GEMV on pre-quantized activations (xq int8 [rows, k],
+ * xs fp32 [rows, k/128]): int32 dot per 128-group, then
+ * acc = acc + (float(p_g) * xs_g) * ws[n, g] in ascending g, no FMA.
+ * Replaces w8a8._linear (w8a8.py:25-41). */
+int lm_w8a8_grouped_gemv(const int8_t *xq, const float *xs,
+                         const int64_t *table, void *y, int64_t experts,
+                         int64_t n, int64_t k, int field, int shared,
+                         void *stream);
+
+/* lm_act_quant_g128 fused into lm_w8a8_grouped_gemv (x bf16).
+ * Replaces w8a8.grouped_linear (w8a8.py:44-48). */
+int lm_w8a8_grouped_linear(const void *x, const int64_t *table, void *y,
+                           int64_t experts, int64_t n, int64_t k, int field,
+                           int shared, void *stream);
+
+/* Exact int32 per-group partials p[m, n, g] = sum_{k in g} xq[m, k] * wq[n, k]
+ * of the W8A8 GEMV inner product (the tl.dot of w8a8.py:37), computed by the
+ * same device code as the GEMV.  Exposed so callers can check bit-exactness. */
+int lm_w8a8_group_partials(const int8_t *xq, const int8_t *wq, int32_t *p,
+                           int64_t m, int64_t n, int64_t k, void *stream);
+
+/* Dense W8A8 decode linear for m <= 8 rows of bf16 x: per-row dynamic
+ * quantization, int32 group dots, the w8a8.py:40 fp32 epilogue, bf16 out.
+ * swiglu != 0 treats the n weight rows as [gate; up] halves and writes
+ * y[m, n/2] = bf16(bf16(silu(gate)) * up) (HF:715, int8.py:182-184).
+ * No reference counterpart as one call: it is w8a8.quantize + w8a8._linear
+ * + the SwiGLU glue on one dense matrix. */
+int lm_w8a8_linear(const void *x, const int8_t *q, const float *s, void *y,
+                   int64_t m, int64_t n, int64_t k, int swiglu, void *stream);
+
+/* bf16 SwiGLU glue: h[r, c] = bf16(bf16(silu(gu[r, c])) * gu[r, half + c]).
+ * Replaces `gate, up = gu.chunk(2, -1); silu(gate) * up`
+ * (int8.py:182-184, prefill.py:77-78, gpu_routes.py:74-75). */
+int lm_swiglu(const void *gu, void *h, int64_t rows, int64_t half,
+              void *stream);
+
+/* Decode combine over the descriptor table, ascending table order:
+ * acc = bf16(acc + bf16(v[e, c] * w[slot_e])).  w_dtype LM_BF16 or LM_FP32.
+ * Replaces int8._ordered_reduce (int8.py:240-250). */
+int lm_ordered_reduce(const void *v, const int64_t *table, const void *w,
+                      int w_dtype, void *y, int64_t n, int64_t experts,
+                      void *stream);
+
+/* Prefill combine: per token over its top_k routes in ascending expert order
+ * acc = bf16(acc + bf16(v[ordered[t,i], c] * w[t, slots[t,i]])).
+ * Replaces prefill._reduce (prefill.py:37-49). */
+int lm_routed_reduce(const void *v, const int64_t *ordered,
+                     const int64_t *slots, const void *w, int w_dtype,
+                     void *y, int64_t tokens, int64_t n, int64_t top_k,
+                     void *stream);
+
+/* Device route plan of gpu_routes.plan + _table (gpu_routes.py:17-36,47-63):
+ * stable sort of the flat ids by expert; pos[p] = token of the p-th sorted
+ * route; table[max_tiles, 3] = (expert, start, stop) per bm-row tile with
+ * surplus rows (0, 0, 0); ordered[t, i] = sorted position of token t's i-th
+ * smallest-id route; slots = argsort(ids, dim=1, stable).  ids int64
+ * [tokens, top_k] in [0, experts).  experts <= 256.  max_tiles must be
+ * ceil(tokens*top_k / bm) + experts. */
+int lm_route_plan(const int64_t *ids, int64_t tokens, int64_t top_k,
+                  int64_t experts, int64_t bm, int64_t *pos, int64_t *table,
+                  int64_t max_tiles, int64_t *ordered, int64_t *slots,
+                  void *stream);
+
+/* Host (CPU) route plan of routing.plan_routes (routing.py:5-20):
+ * positions[2, R] = (sorted_route // top_k, sorted_route % top_k) and the
+ * segments (expert, start, stop) of non-empty experts; *n_segments receives
+ * their count (segments arrays need room for `experts`).  Returns LM_EINVAL
+ * for an empty input or an out-of-range id. */
+int lm_plan_routes_host(const int64_t *ids, int64_t tokens, int64_t top_k,
+                        int64_t experts, int64_t *positions,
+                        int64_t *seg_expert, int64_t *seg_start,
+                        int64_t *seg_stop, int64_t *n_segments);
+
+/* Routed grouped W8A16 GEMM over a tile table (MFMA): for each tile
+ * (e, start, stop) rows r in [start, min(start+bm, stop)):
+ * y[r, :] = x[gather ? pos[r] : r, :] . dequant(q[e], s[e])^T.
+ * bm must equal the table's tile height (<= 128).  Strides are in elements.
+ * Replaces prefill._routed / gpu_routes._nonempty (prefill.py:12-34,
+ * gpu_routes.py:39-44). */
+int lm_routed_gemm_w8a16(const void *x, const int8_t *q, const float *s,
+                         const int64_t *pos, const int64_t *table,
+                         int64_t n_tiles, int64_t bm, void *y, int64_t n,
+                         int64_t k, int gather, int64_t q_expert_stride,
+                         int64_t s_expert_stride, void *stream);
+
+/* lm_routed_gemm_w8a16 on the gate_up bank with the SwiGLU glue fused into
+ * the epilogue: h[r, c] = bf16(bf16(silu(gu[r, c])) * gu[r, n/2 + c]),
+ * h is [rows, n/2].  Same result as prefill.py:75-78 without the [R, n]
+ * intermediate. */
+int lm_routed_gate_up_swiglu(const void *x, const int8_t *q, const float *s,
+                             const int64_t *pos, const int64_t *table,
+                             int64_t n_tiles, int64_t bm, void *h, int64_t n,
+                             int64_t k, int64_t q_expert_stride,
+                             int64_t s_expert_stride, void *stream);
+
+/* HF Qwen3_5MoeTopKRouter (HF:768-776) with a fixed tie rule:
+ * logits[t, e] = float(bf16(float(sum_k double(x[t,k]) * double(w[e,k]))))
+ * (+ bias[e] if bias != NULL, fp32 add); ids = top_k experts by
+ * (logit desc, expert id asc); p = fp32 softmax over all experts;
+ * weights = bf16(p_sel / sum(p_sel)).  ids are written in selection order.
+ * x, w bf16; logits fp32 [tokens, experts] (required); ids int64
+ * [tokens, top_k]; weights bf16 [tokens, top_k].  experts <= 256,
+ * top_k <= 16. */
+int lm_router_topk(const void *x, const void *w, const float *bias,
+                   float *logits, int64_t *ids, void *weights, int64_t tokens,
+                   int64_t experts, int64_t hidden, int64_t top_k,
+                   void *stream);
+
+/* Qwen3_5MoeRMSNorm (HF:801-815): y = bf16(x * rsqrt(mean(x^2) + eps)
+ * * (1 + w)); x, y bf16 [rows, n], w fp32 [n] (NULL = zeros). */
+int lm_rmsnorm(const void *x, const float *w, void *y, int64_t rows,
+               int64_t n, float eps, void *stream);
+
+/* ---------------------------------------------------------------------
+ * Fused MoE-FFN block of the synthetic stack (router + 256 routed experts
+ * top-8 + shared expert + RMSNorm + residual; HF:779-798, 801-815, 866-875).
+ * One layer's weights:
+ *   router_w  bf16 [E, H]         shared_gate_w bf16 [H]
+ *   norm_w    fp32 [H] or NULL    router_bias fp32 [E] or NULL
+ *   gu_q int8 [E+1, 2I, H], gu_s fp32 [E+1, 2I, H/128]   (index E = shared)
+ *   dn_q int8 [E+1, H, I],  dn_s fp32 [E+1, H, I/128]
+ * h bf16 [tokens, H] is the residual stream, updated in place:
+ *   h = bf16(h + bf16(routed + bf16(bf16(sigmoid(g)) * shared)))
+ * Decode (tokens == 1) runs routed experts W8A8 (w8a8.py) and the shared
+ * expert W8A16; prefill runs everything W8A16 (prefill.py / gpu_routes.py).
+ * H = 2048, I = 512, E = 256, top_k = 8 are the supported geometry.
+ * `workspace` is caller-owned device memory of lm_moe_workspace_bytes();
+ * it must start zeroed once (lm_moe_workspace_init) and is reused by every
+ * later call on the same stream.  Calls sharing a workspace must not
+ * overlap. */
+typedef struct lm_moe_layer {
+  const void *router_w;
+  const float *router_bias;
+  const void *shared_gate_w;
+  const float *norm_w;
+  const int8_t *gu_q;
+  const float *gu_s;
+  const int8_t *dn_q;
+  const float *dn_s;
+  int64_t gu_q_expert_stride; /* elements between experts of gu_q */
+  int64_t gu_s_expert_stride;
+  int64_t dn_q_expert_stride;
+  int64_t dn_s_expert_stride;
+} lm_moe_layer;
+
+int64_t lm_moe_workspace_bytes(int64_t max_tokens, int64_t hidden,
+                               int64_t inter, int64_t experts, int64_t top_k);
+int lm_moe_workspace_init(void *workspace, int64_t bytes, void *stream);
+
+/* One MoE-FFN layer on `tokens` rows of h (decode path when tokens == 1).
+ * If ids_out / weights_out are non-NULL the routing of this layer is copied
+ * there (int32 [tokens, top_k] in selection order, bf16 [tokens, top_k]).
+ * phase_events, if non-NULL, holds hipEvent_t handles recorded on `stream`
+ * before each kernel phase and after the last one: 8 for prefill (norm+gate,
+ * router logits, top-k, plan, gate_up, down, combine, end), 4 for decode
+ * (router, gate_up, down, end). */
+int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t tokens,
+                         int64_t hidden, int64_t inter, int64_t experts,
+                         int64_t top_k, float eps, void *workspace,
+                         int64_t workspace_bytes, int32_t *ids_out,
+                         void *weights_out, void *const *phase_events,
+                         void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LOCALMOE35BA3B_H */

@@ -1,0 +1,384 @@
+// Decode GEMV kernels behind the generic operator entry points:
+//   lm_w8a8_grouped_gemv / lm_w8a8_grouped_linear   (w8a8.py:25-48)
+//   lm_w8a8_linear (dense, optional SwiGLU)          (config: W8A8 gate_up)
+//   lm_w8a8_group_partials                           (exact int32 partials)
+//   lm_w8a16_grouped_gemv                            (int8.py:213-237)
+//   lm_w8a16_linear for m <= 8                       (int8.py:9-37)
+// All of them stream the weights with gemv_core.hpp; blockIdx.y selects the
+// expert of a descriptor table (grouped mode) or is 0 (dense mode).
+#include "gemv_core.hpp"
+
+namespace lm {
+
+constexpr int kGemvThreads = 256;
+constexpr int kGemvLoads = 8;
+
+struct GemvArgs {
+  const int64_t *table;  // grouped mode: [experts, 5] descriptor rows
+  int field;
+  int shared;
+  const int8_t *q;  // dense mode weights [N, K] and scales [N, G]
+  const float *s;
+  const uint16_t *x;  // 16-bit activations [M, ldx]
+  int64_t ldx;
+  const int8_t *xq;  // pre-quantized activations [M, K] / [M, G]
+  const float *xs;
+  int M;
+  uint16_t *y;  // output [M or experts, ldy]
+  int64_t ldy;
+  int32_t *partials;  // [M, N, G] (partials mode)
+  int N;
+  int K;
+  int RB;  // weight rows per block (before SwiGLU pairing)
+  int swiglu;
+};
+
+struct Resolved {
+  const int8_t *q;
+  const float *s;
+  int xrow;   // first activation row used by this block
+  int yrow;   // first output row written by this block
+  int n0;     // first output column
+  int rvalid; // rows streamed by this block
+  RowMap map;
+};
+
+__device__ __forceinline__ Resolved resolve(const GemvArgs &a) {
+  Resolved r;
+  const int e = blockIdx.y;
+  if (a.table) {
+    r.q = reinterpret_cast<const int8_t *>(a.table[e * 5 + a.field]);
+    r.s = reinterpret_cast<const float *>(a.table[e * 5 + a.field + 1]);
+    r.xrow = a.shared ? 0 : e;
+    r.yrow = e;
+  } else {
+    r.q = a.q;
+    r.s = a.s;
+    r.xrow = 0;
+    r.yrow = 0;
+  }
+  if (a.swiglu) {
+    const int half = a.N >> 1;
+    const int hb = a.RB >> 1;
+    r.n0 = blockIdx.x * hb;
+    const int rh = min(hb, half - r.n0);
+    r.rvalid = 2 * rh;
+    r.map = RowMap{r.n0, half + r.n0, rh};
+  } else {
+    r.n0 = blockIdx.x * a.RB;
+    r.rvalid = min(a.RB, a.N - r.n0);
+    r.map = RowMap{r.n0, 0, 0};
+  }
+  return r;
+}
+
+// LDS carve-up: [xq or x16 | xs | ws | partials]
+template <int MT, bool QUANT, bool PARTIALS>
+__global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const Resolved rv = resolve(a);
+  const int K = a.K, G = K >> 7, M = a.M;
+  int8_t *xq = reinterpret_cast<int8_t *>(smem);
+  float *xs = reinterpret_cast<float *>(smem + MT * K);
+  float *ws = xs + MT * G;
+  int *part = reinterpret_cast<int *>(ws + a.RB * G);
+  const int RG = a.RB * G;
+
+  // Activations: quantize bf16 rows, or copy pre-quantized rows.
+  if constexpr (QUANT) {
+    quantize_rows_to_lds<BF16>(a.x + (int64_t)rv.xrow * a.ldx, a.ldx, M, K, xq, xs);
+  } else {
+    for (int i = threadIdx.x; i < M * K / 16; i += blockDim.x) {
+      const int m = (i * 16) / K, c = (i * 16) - m * K;
+      *reinterpret_cast<u32x4 *>(xq + m * K + c) =
+          ldg16(a.xq + (int64_t)(rv.xrow + m) * K + c);
+    }
+    if (a.xs)
+      for (int i = threadIdx.x; i < M * G; i += blockDim.x)
+        xs[i] = a.xs[(int64_t)(rv.xrow + i / G) * G + i % G];
+  }
+  if constexpr (!PARTIALS) {
+    for (int i = threadIdx.x; i < rv.rvalid * G; i += blockDim.x) {
+      const int r = i / G, g = i - r * G;
+      ws[i] = rv.s[(int64_t)rv.map(r) * G + g];
+    }
+  }
+  __syncthreads();
+
+  const int8_t *q = rv.q;
+  auto row_ptr = [&](int r) { return q + (int64_t)rv.map(r) * K; };
+  const int sub = threadIdx.x & 7;
+  stream_rows<kGemvLoads>(rv.rvalid, G, row_ptr, [&](u32x4 w, int r, int g, int f, bool ok) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < M) {
+        const u32x4 xv = *reinterpret_cast<const u32x4 *>(xq + m * K + g * 128 + sub * 16);
+        const int p = octet_sum_i32(dot16_i8(w, xv));
+        if (ok && sub == 0) part[m * RG + f] = p;
+      }
+    }
+  });
+  __syncthreads();
+
+  if constexpr (PARTIALS) {
+    for (int i = threadIdx.x; i < M * rv.rvalid * G; i += blockDim.x) {
+      const int m = i / (rv.rvalid * G);
+      const int f = i - m * rv.rvalid * G;
+      const int r = f / G, g = f - r * G;
+      a.partials[((int64_t)m * a.N + rv.map(r)) * G + g] = part[m * RG + f];
+    }
+    return;
+  } else {
+    if (a.swiglu) {
+      const int rh = rv.rvalid >> 1;
+      for (int i = threadIdx.x; i < M * rh; i += blockDim.x) {
+        const int m = i / rh, t = i - m * rh;
+        const float gate = round_bf16(w8a8_epilogue(part + m * RG + t * G, xs + m * G, ws + t * G, G));
+        const float up =
+            round_bf16(w8a8_epilogue(part + m * RG + (rh + t) * G, xs + m * G, ws + (rh + t) * G, G));
+        const float act = round_bf16(silu_f32(gate));
+        a.y[(int64_t)(rv.yrow + m) * a.ldy + rv.n0 + t] = f32_to_bf16_bits(act * up);
+      }
+    } else {
+      for (int i = threadIdx.x; i < M * rv.rvalid; i += blockDim.x) {
+        const int m = i / rv.rvalid, t = i - m * rv.rvalid;
+        const float acc = w8a8_epilogue(part + m * RG + t * G, xs + m * G, ws + t * G, G);
+        a.y[(int64_t)(rv.yrow + m) * a.ldy + rv.n0 + t] = f32_to_bf16_bits(acc);
+      }
+    }
+  }
+}
+
+// W8A16: dequantize to T exactly (T(q * s)), fp32 dot products.
+// LDS carve-up: [x16 rows | ws | partials]
+template <typename T, int MT>
+__global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const Resolved rv = resolve(a);
+  const int K = a.K, G = K >> 7, M = a.M;
+  uint16_t *xl = reinterpret_cast<uint16_t *>(smem);
+  float *ws = reinterpret_cast<float *>(smem + MT * K * 2);
+  float *part = ws + a.RB * G;
+  const int RG = a.RB * G;
+
+  for (int i = threadIdx.x; i < M * K / 8; i += blockDim.x) {
+    const int m = (i * 8) / K, c = (i * 8) - m * K;
+    *reinterpret_cast<u32x4 *>(xl + m * K + c) = ldg16(a.x + (int64_t)(rv.xrow + m) * a.ldx + c);
+  }
+  for (int i = threadIdx.x; i < rv.rvalid * G; i += blockDim.x) {
+    const int r = i / G, g = i - r * G;
+    ws[i] = rv.s[(int64_t)rv.map(r) * G + g];
+  }
+  __syncthreads();
+
+  const int8_t *q = rv.q;
+  auto row_ptr = [&](int r) { return q + (int64_t)rv.map(r) * K; };
+  const int sub = threadIdx.x & 7;
+  stream_rows<kGemvLoads>(rv.rvalid, G, row_ptr, [&](u32x4 w, int r, int g, int f, bool ok) {
+    uint32_t wd[8];
+    dequant16<T>(w, ok ? ws[f] : 0.0f, wd);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < M) {
+        const uint16_t *xp = xl + m * K + g * 128 + sub * 16;
+        const u32x4 x0 = *reinterpret_cast<const u32x4 *>(xp);
+        const u32x4 x1 = *reinterpret_cast<const u32x4 *>(xp + 8);
+        const float p = octet_sum_f32(dot16_w16<T>(wd, x0, x1));
+        if (ok && sub == 0) part[m * RG + f] = p;
+      }
+    }
+  });
+  __syncthreads();
+
+  for (int i = threadIdx.x; i < M * rv.rvalid; i += blockDim.x) {
+    const int m = i / rv.rvalid, t = i - m * rv.rvalid;
+    float acc = 0.0f;
+    for (int g = 0; g < G; ++g) acc += part[m * RG + t * G + g];
+    a.y[(int64_t)(rv.yrow + m) * a.ldy + rv.n0 + t] = T::from_f32(acc);
+  }
+}
+
+// Rows per block: about 32 KB of weights (8 loads in flight per lane).
+static int gemv_rows_per_block(int64_t k) {
+  int rb = (int)(32768 / k);
+  if (rb < 2) rb = 2;
+  if (rb > 256) rb = 256;
+  rb &= ~1;
+  return rb;
+}
+
+static int mt_for(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; }
+
+template <int MT, bool QUANT, bool PARTIALS>
+static int launch_w8a8(const GemvArgs &a, unsigned gy, hipStream_t st) {
+  const int G = a.K / 128;
+  const size_t lds = (size_t)MT * a.K + (size_t)MT * G * 4 + (size_t)a.RB * G * 4 +
+                     (size_t)MT * a.RB * G * 4;
+  LM_REQUIRE(lds <= 160 * 1024, LM_EINVAL, "Invalid INT8 group geometry");
+  const unsigned gx = a.swiglu ? cdiv(a.N / 2, a.RB / 2) : cdiv(a.N, a.RB);
+  w8a8_gemv_kernel<MT, QUANT, PARTIALS><<<dim3(gx, gy), kGemvThreads, lds, st>>>(a);
+  return check_launch("w8a8_gemv_kernel");
+}
+
+template <bool QUANT, bool PARTIALS>
+static int dispatch_w8a8(const GemvArgs &a, unsigned gy, hipStream_t st) {
+  switch (mt_for(a.M)) {
+    case 1: return launch_w8a8<1, QUANT, PARTIALS>(a, gy, st);
+    case 2: return launch_w8a8<2, QUANT, PARTIALS>(a, gy, st);
+    case 4: return launch_w8a8<4, QUANT, PARTIALS>(a, gy, st);
+    default: return launch_w8a8<8, QUANT, PARTIALS>(a, gy, st);
+  }
+}
+
+template <typename T, int MT>
+static int launch_w8a16(const GemvArgs &a, unsigned gy, hipStream_t st) {
+  const int G = a.K / 128;
+  const size_t lds = (size_t)MT * a.K * 2 + (size_t)a.RB * G * 4 + (size_t)MT * a.RB * G * 4;
+  LM_REQUIRE(lds <= 160 * 1024, LM_EINVAL, "Invalid INT8 group geometry");
+  const unsigned gx = cdiv(a.N, a.RB);
+  w8a16_gemv_kernel<T, MT><<<dim3(gx, gy), kGemvThreads, lds, st>>>(a);
+  return check_launch("w8a16_gemv_kernel");
+}
+
+template <typename T>
+static int dispatch_w8a16(const GemvArgs &a, unsigned gy, hipStream_t st) {
+  switch (mt_for(a.M)) {
+    case 1: return launch_w8a16<T, 1>(a, gy, st);
+    case 2: return launch_w8a16<T, 2>(a, gy, st);
+    case 4: return launch_w8a16<T, 4>(a, gy, st);
+    default: return launch_w8a16<T, 8>(a, gy, st);
+  }
+}
+
+int w8a16_gemv_dense(const void *x, const int8_t *q, const float *s, void *y, int64_t m,
+                     int64_t n, int64_t k, int dtype, hipStream_t st) {
+  GemvArgs a{};
+  a.q = q;
+  a.s = s;
+  a.x = static_cast<const uint16_t *>(x);
+  a.ldx = k;
+  a.M = (int)m;
+  a.y = static_cast<uint16_t *>(y);
+  a.ldy = n;
+  a.N = (int)n;
+  a.K = (int)k;
+  a.RB = gemv_rows_per_block(k);
+  return dtype == LM_BF16 ? dispatch_w8a16<BF16>(a, 1, st) : dispatch_w8a16<FP16>(a, 1, st);
+}
+
+}  // namespace lm
+
+using namespace lm;
+
+static int check_grouped(int64_t experts, int64_t n, int64_t k, int field) {
+  LM_REQUIRE(experts >= 0 && n > 0 && k > 0 && k % 128 == 0 && k <= 65536, LM_EINVAL,
+             "Invalid INT8 group geometry");
+  LM_REQUIRE(field == 0 || field == 2, LM_EINVAL, "descriptor field must be 0 or 2");
+  LM_REQUIRE(n <= (1 << 24), LM_EINVAL, "Invalid INT8 group geometry");
+  return LM_OK;
+}
+
+extern "C" int lm_w8a8_grouped_gemv(const int8_t *xq, const float *xs, const int64_t *table,
+                                    void *y, int64_t experts, int64_t n, int64_t k, int field,
+                                    int shared, void *stream) {
+  if (int rc = check_grouped(experts, n, k, field)) return rc;
+  if (experts == 0) return LM_OK;
+  LM_REQUIRE(xq && xs && table && y, LM_EINVAL, "null pointer");
+  GemvArgs a{};
+  a.table = table;
+  a.field = field;
+  a.shared = shared;
+  a.xq = xq;
+  a.xs = xs;
+  a.M = 1;
+  a.y = static_cast<uint16_t *>(y);
+  a.ldy = n;
+  a.N = (int)n;
+  a.K = (int)k;
+  a.RB = gemv_rows_per_block(k);
+  return dispatch_w8a8<false, false>(a, (unsigned)experts, as_stream(stream));
+}
+
+extern "C" int lm_w8a8_grouped_linear(const void *x, const int64_t *table, void *y,
+                                      int64_t experts, int64_t n, int64_t k, int field,
+                                      int shared, void *stream) {
+  if (int rc = check_grouped(experts, n, k, field)) return rc;
+  if (experts == 0) return LM_OK;
+  LM_REQUIRE(x && table && y, LM_EINVAL, "null pointer");
+  GemvArgs a{};
+  a.table = table;
+  a.field = field;
+  a.shared = shared;
+  a.x = static_cast<const uint16_t *>(x);
+  a.ldx = k;
+  a.M = 1;
+  a.y = static_cast<uint16_t *>(y);
+  a.ldy = n;
+  a.N = (int)n;
+  a.K = (int)k;
+  a.RB = gemv_rows_per_block(k);
+  return dispatch_w8a8<true, false>(a, (unsigned)experts, as_stream(stream));
+}
+
+extern "C" int lm_w8a8_linear(const void *x, const int8_t *q, const float *s, void *y, int64_t m,
+                              int64_t n, int64_t k, int swiglu, void *stream) {
+  LM_REQUIRE(m >= 0 && m <= 8, LM_EINVAL, "W8A8 decode linear supports 1..8 rows");
+  LM_REQUIRE(n > 0 && k > 0 && k % 128 == 0 && k <= 65536, LM_EINVAL,
+             "Invalid INT8 group geometry");
+  LM_REQUIRE(!swiglu || n % 2 == 0, LM_EINVAL, "SwiGLU needs an even number of rows");
+  if (m == 0) return LM_OK;
+  LM_REQUIRE(x && q && s && y, LM_EINVAL, "null pointer");
+  GemvArgs a{};
+  a.q = q;
+  a.s = s;
+  a.x = static_cast<const uint16_t *>(x);
+  a.ldx = k;
+  a.M = (int)m;
+  a.y = static_cast<uint16_t *>(y);
+  a.ldy = swiglu ? n / 2 : n;
+  a.N = (int)n;
+  a.K = (int)k;
+  a.RB = gemv_rows_per_block(k);
+  a.swiglu = swiglu ? 1 : 0;
+  return dispatch_w8a8<true, false>(a, 1, as_stream(stream));
+}
+
+extern "C" int lm_w8a8_group_partials(const int8_t *xq, const int8_t *wq, int32_t *p, int64_t m,
+                                      int64_t n, int64_t k, void *stream) {
+  LM_REQUIRE(m >= 0 && m <= 8, LM_EINVAL, "W8A8 partials support 1..8 rows");
+  LM_REQUIRE(n > 0 && k > 0 && k % 128 == 0 && k <= 65536, LM_EINVAL,
+             "Invalid INT8 group geometry");
+  if (m == 0) return LM_OK;
+  LM_REQUIRE(xq && wq && p, LM_EINVAL, "null pointer");
+  GemvArgs a{};
+  a.q = wq;
+  a.xq = xq;
+  a.xs = nullptr;
+  a.M = (int)m;
+  a.partials = p;
+  a.N = (int)n;
+  a.K = (int)k;
+  a.RB = gemv_rows_per_block(k);
+  return dispatch_w8a8<false, true>(a, 1, as_stream(stream));
+}
+
+extern "C" int lm_w8a16_grouped_gemv(const void *x, const int64_t *table, void *y,
+                                     int64_t experts, int64_t n, int64_t k, int field, int shared,
+                                     void *stream) {
+  if (int rc = check_grouped(experts, n, k, field)) return rc;
+  if (experts == 0) return LM_OK;
+  LM_REQUIRE(x && table && y, LM_EINVAL, "null pointer");
+  GemvArgs a{};
+  a.table = table;
+  a.field = field;
+  a.shared = shared;
+  a.x = static_cast<const uint16_t *>(x);
+  a.ldx = k;
+  a.M = 1;
+  a.y = static_cast<uint16_t *>(y);
+  a.ldy = n;
+  a.N = (int)n;
+  a.K = (int)k;
+  a.RB = gemv_rows_per_block(k);
+  return dispatch_w8a16<BF16>(a, (unsigned)experts, as_stream(stream));
+}

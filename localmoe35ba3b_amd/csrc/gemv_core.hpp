@@ -1,0 +1,185 @@
+// Streaming int8-weight GEMV core for decode (M <= 8 activation rows).
+//
+// A block streams R weight rows of K int8 each.  The (row, 128-group) pairs
+// are flattened to f = r * G + g (G = K / 128); one wave instruction loads
+// 8 consecutive pairs = 1 KB with one 16-byte load per lane, lane octet
+// j = lane / 8 covering pair 8 i + j.  Each wave owns a contiguous run of
+// instructions and issues a whole batch of loads before consuming any of
+// them, so a block keeps LOADS * 4 KB of weights in flight.  Per-pair
+// partial dot products are reduced across the octet with DPP and parked in
+// LDS; the per-row epilogue then walks the groups in ascending order, which
+// is what the W8A8 reference epilogue requires (w8a8.py:40).
+#pragma once
+#include "common.hpp"
+
+namespace lm {
+
+// Row index -> weight row.  `split` > 0 maps rows [0, split) to
+// first + r and rows [split, 2 split) to second + (r - split): the gate / up
+// halves of a fused gate_up matrix.
+struct RowMap {
+  int first;
+  int second;
+  int split;
+  __device__ __forceinline__ int operator()(int r) const {
+    return (split > 0 && r >= split) ? second + (r - split) : first + r;
+  }
+};
+
+// Walks this wave's instructions in batches of LOADS.  `body(w, r, g, f, ok)`
+// receives each lane's 16 bytes of row r, group g (flattened index f); ok is
+// false for lanes past the end (their w is zero).  All lanes of the wave
+// call body together, so body may use cross-lane DPP.
+template <int LOADS, typename RowPtr, typename Body>
+__device__ __forceinline__ void stream_rows(int R, int G, RowPtr row_ptr, Body body) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  const int oct = lane >> 3;
+  const int sub = lane & 7;
+  const int total = R * G;
+  const int ninstr = (total + 7) >> 3;
+  const int ipw = (ninstr + nwaves - 1) / nwaves;
+  const int ibeg = wave * ipw;
+  const int iend = min(ibeg + ipw, ninstr);
+  int f = ibeg * 8 + oct;
+  int r = f / G;
+  int g = f - r * G;
+  for (int i = ibeg; i < iend; i += LOADS) {
+    u32x4 w[LOADS];
+    int rs[LOADS], gs[LOADS], fs[LOADS];
+    bool ok[LOADS];
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      ok[u] = (i + u < iend) && (f < total);
+      rs[u] = r;
+      gs[u] = g;
+      fs[u] = f;
+      if (ok[u]) {
+        w[u] = ldg16(row_ptr(r) + g * 128 + sub * 16);
+      } else {
+        w[u] = u32x4{0u, 0u, 0u, 0u};
+      }
+      f += 8;
+      g += 8;
+      while (g >= G) {
+        g -= G;
+        ++r;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) body(w[u], rs[u], gs[u], fs[u], ok[u]);
+  }
+}
+
+// One-batch form of stream_rows for kernels whose waves own at most LOADS
+// instructions: issue() starts every load of the wave, consume() runs the
+// body afterwards, so a prologue placed between the two overlaps the HBM
+// latency.
+template <int LOADS>
+struct RowLoads {
+  u32x4 w[LOADS];
+  int r[LOADS], g[LOADS], f[LOADS];
+  bool ok[LOADS];
+
+  template <typename RowPtr>
+  __device__ __forceinline__ void issue(int R, int G, RowPtr row_ptr) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int nwaves = blockDim.x >> 6;
+    const int sub = lane & 7;
+    const int total = R * G;
+    const int ninstr = (total + 7) >> 3;
+    const int ipw = (ninstr + nwaves - 1) / nwaves;
+    const int ibeg = wave * ipw;
+    const int iend = min(ibeg + ipw, ninstr);
+    int ff = ibeg * 8 + (lane >> 3);
+    int rr = ff / G;
+    int gg = ff - rr * G;
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) {
+      ok[u] = (ibeg + u < iend) && (ff < total);
+      r[u] = rr;
+      g[u] = gg;
+      f[u] = ff;
+      w[u] = ok[u] ? ldg16(row_ptr(rr) + gg * 128 + sub * 16) : u32x4{0u, 0u, 0u, 0u};
+      ff += 8;
+      gg += 8;
+      while (gg >= G) {
+        gg -= G;
+        ++rr;
+      }
+    }
+  }
+
+  template <typename Body>
+  __device__ __forceinline__ void consume(Body body) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) body(w[u], r[u], g[u], f[u], ok[u]);
+  }
+};
+
+// Per-row dynamic quantization of `rows` activation rows of K 16-bit values
+// into LDS (w8a8.py:8-14).  Each 128-group is handled by 32 lanes.
+template <typename T>
+__device__ __forceinline__ void quantize_rows_to_lds(const uint16_t *x, int64_t ldx, int rows,
+                                                     int K, int8_t *xq, float *xs) {
+  const int G = K >> 7;
+  const int half = threadIdx.x >> 5;
+  const int nhalf = blockDim.x >> 5;
+  const int l = threadIdx.x & 31;
+  const float inv127 = (float)(1.0 / 127.0);
+  for (int job = half; job < rows * G; job += nhalf) {
+    const int m = job / G;
+    const int g = job - m * G;
+    const uint2 raw = *reinterpret_cast<const uint2 *>(x + m * ldx + g * 128 + l * 4);
+    float v[4] = {T::to_f32(raw.x & 0xFFFFu), T::to_f32(raw.x >> 16), T::to_f32(raw.y & 0xFFFFu),
+                  T::to_f32(raw.y >> 16)};
+    float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+    const float sc = fmaxf(a, 1e-10f) * inv127;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[i] / sc)) << (8 * i);
+    *reinterpret_cast<uint32_t *>(xq + m * K + g * 128 + l * 4) = packed;
+    if (l == 0) xs[m * G + g] = sc;
+  }
+}
+
+// Sixteen int8 weights against sixteen int8 activations: exact int32.
+__device__ __forceinline__ int dot16_i8(u32x4 w, u32x4 x) {
+  int p = __builtin_amdgcn_sdot4((int)w[0], (int)x[0], 0, false);
+  p = __builtin_amdgcn_sdot4((int)w[1], (int)x[1], p, false);
+  p = __builtin_amdgcn_sdot4((int)w[2], (int)x[2], p, false);
+  p = __builtin_amdgcn_sdot4((int)w[3], (int)x[3], p, false);
+  return p;
+}
+
+// Sixteen dequantized weights (8 packed words) against sixteen 16-bit
+// activations (two 16-byte vectors), fp32 accumulate.
+template <typename T>
+__device__ __forceinline__ float dot16_w16(const uint32_t wd[8], u32x4 x0, u32x4 x1) {
+  float a = 0.0f;
+  a = T::dot2(wd[0], x0[0], a);
+  a = T::dot2(wd[1], x0[1], a);
+  a = T::dot2(wd[2], x0[2], a);
+  a = T::dot2(wd[3], x0[3], a);
+  a = T::dot2(wd[4], x1[0], a);
+  a = T::dot2(wd[5], x1[1], a);
+  a = T::dot2(wd[6], x1[2], a);
+  a = T::dot2(wd[7], x1[3], a);
+  return a;
+}
+
+// The W8A8 reference epilogue over one row's group partials (w8a8.py:40):
+// acc = acc + (float(p_g) * xs_g) * ws_g for g ascending, no FMA.
+__device__ __forceinline__ float w8a8_epilogue(const int *p, const float *xs, const float *ws,
+                                               int G) {
+  float acc = 0.0f;
+  for (int g = 0; g < G; ++g) acc = add_rn(acc, mul_rn(mul_rn((float)p[g], xs[g]), ws[g]));
+  return acc;
+}
+
+}  // namespace lm

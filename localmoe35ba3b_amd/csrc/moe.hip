@@ -1,0 +1,564 @@
+// Fused MoE-FFN layer of the synthetic stack: RMSNorm -> router top-8 ->
+// 8 routed experts + the always-on shared expert -> weighted combine ->
+// sigmoid-gated shared add -> residual (HF:779-798, 801-815, 866-875).
+//
+// Decode (one token) runs three kernels and never leaves the device:
+//   decode_router_kernel   RMSNorm, fp64 router logits (one wave per expert),
+//                          activation quantization of the normalized row, the
+//                          shared-expert gate; the last workgroup to finish
+//                          runs top-8 + softmax renormalisation.
+//   decode_gate_up_kernel  gate_up rows of the 8 routed experts (W8A8,
+//                          w8a8.py) and of the shared expert (W8A16), SwiGLU.
+//   decode_down_kernel     down rows of all 9 experts for 8 output columns,
+//                          W8A8 (row-quantized SwiGLU output) / W8A16, then the
+//                          ascending-expert bf16 combine (int8.py:240-250), the
+//                          gated shared add and the residual add, in place.
+// Prefill runs: RMSNorm + shared gate, router (fp64 MFMA), top-k, device route
+// plan (with the shared expert appended as extra tiles), grouped W8A16 gate_up
+// GEMM with fused SwiGLU, grouped W8A16 down GEMM, and a per-token combine.
+#include "gemv_core.hpp"
+#include "internal.hpp"
+
+namespace lm {
+
+constexpr int kH = 2048;
+constexpr int kI = 512;
+constexpr int kE = 256;
+constexpr int kTopK = 8;
+constexpr int kBM = 64;  // prefill MFMA tile height
+
+struct WsLayout {
+  int64_t ctr, xn, gl, logits, ids, wts, sel, selw, xq, xs, pos, table, ordered, slots, hbuf,
+      vbuf, total;
+  int64_t max_tiles, n_tiles;
+};
+
+static int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
+
+static WsLayout layout(int64_t T) {
+  WsLayout w{};
+  const int64_t R = T * kTopK;
+  w.max_tiles = (R + kBM - 1) / kBM + kE;
+  w.n_tiles = w.max_tiles + (T + kBM - 1) / kBM;
+  int64_t o = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = o;
+    o = align256(o + bytes);
+    return at;
+  };
+  w.ctr = take(256);
+  w.xn = take(T * kH * 2);
+  w.gl = take(T * 4);
+  w.logits = take(T * kE * 4);
+  w.ids = take(T * kTopK * 8);
+  w.wts = take(T * kTopK * 2);
+  w.sel = take(kTopK * 4);
+  w.selw = take(kTopK * 4);
+  w.xq = take(kH);
+  w.xs = take(kH / 128 * 4);
+  w.pos = take((R + T) * 8);
+  w.table = take(w.n_tiles * 3 * 8);
+  w.ordered = take(R * 8);
+  w.slots = take(R * 8);
+  w.hbuf = take((R + T) * kI * 2);
+  w.vbuf = take((R + T) * kH * 2);
+  w.total = o;
+  return w;
+}
+
+struct LayerArgs {
+  const uint16_t *router_w;
+  const float *router_bias;
+  const uint16_t *gate_w;
+  const float *norm_w;
+  const int8_t *gu_q;
+  const float *gu_s;
+  const int8_t *dn_q;
+  const float *dn_s;
+  int64_t gu_qes, gu_ses, dn_qes, dn_ses;
+  uint16_t *h;
+  float eps;
+  // workspace views
+  int *ctr;
+  uint16_t *xn;
+  float *gl;
+  float *logits;
+  int64_t *ids;
+  uint16_t *wts;
+  int *sel;
+  float *selw;
+  int8_t *xq;
+  float *xs;
+  uint16_t *hbuf;
+  int32_t *ids_out;
+  uint16_t *wts_out;
+};
+
+// ------------------------------------------------------------------ decode
+// RMSNorm of one row of kH bf16 values into LDS floats (bf16-rounded values).
+__device__ __forceinline__ void norm_row_to_lds(const uint16_t *h, const float *nw, float eps,
+                                                float *xf, float *red) {
+  constexpr int PER = kH / 256;
+  const int t = threadIdx.x;
+  float v[PER];
+  const u32x4 raw = ldg16(h + t * PER);
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = bf16_bits_to_f32(raw[j] & 0xFFFFu);
+    v[2 * j + 1] = bf16_bits_to_f32(raw[j] >> 16);
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) ss += v[j] * v[j];
+  ss = wave_sum_f32(ss);
+  if ((t & 63) == 0) red[t >> 6] = ss;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  const float r = 1.0f / sqrtf(tot / (float)kH + eps);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    float y = v[j] * r;
+    if (nw) y = y * (1.0f + nw[t * PER + j]);
+    xf[t * PER + j] = round_bf16(y);
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ double dot_lds_f64(const float *xf, const uint16_t *w, int lane) {
+  double acc = 0.0;
+#pragma unroll
+  for (int k0 = lane * 8; k0 < kH; k0 += 512) {
+    const u32x4 wv = ldg16(w + k0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc = __builtin_fma((double)xf[k0 + 2 * j], (double)bf16_bits_to_f32(wv[j] & 0xFFFFu), acc);
+      acc = __builtin_fma((double)xf[k0 + 2 * j + 1], (double)bf16_bits_to_f32(wv[j] >> 16), acc);
+    }
+  }
+  return wave_sum_f64(acc);
+}
+
+__global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
+  __shared__ float xf[kH];
+  __shared__ float red[4];
+  __shared__ float lgs[kE];
+  __shared__ int64_t sid[kTopK];
+  __shared__ uint16_t swt[kTopK];
+  __shared__ int is_last;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  norm_row_to_lds(a.h, a.norm_w, a.eps, xf, red);
+
+  if (blockIdx.x < kE / 4) {
+    const int e = blockIdx.x * 4 + wave;
+    const double s = dot_lds_f64(xf, a.router_w + (int64_t)e * kH, lane);
+    if (lane == 0) {
+      float l = round_bf16((float)s);
+      if (a.router_bias) l = l + a.router_bias[e];
+      a.logits[e] = l;
+    }
+  } else {
+    // normalized row, its W8A8 quantization, and the shared-expert gate logit
+    for (int i = t; i < kH; i += 256) a.xn[i] = f32_to_bf16_bits(xf[i]);
+    const int half = t >> 5, l = t & 31;
+    const float inv127 = (float)(1.0 / 127.0);
+    for (int g = half; g < kH / 128; g += 8) {
+      float v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = xf[g * 128 + l * 4 + j];
+      float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+      const float sc = fmaxf(am, 1e-10f) * inv127;
+      uint32_t packed = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[j] / sc)) << (8 * j);
+      *reinterpret_cast<uint32_t *>(a.xq + g * 128 + l * 4) = packed;
+      if (l == 0) a.xs[g] = sc;
+    }
+    if (wave == 0) {
+      const double s = dot_lds_f64(xf, a.gate_w, lane);
+      if (lane == 0) a.gl[0] = round_bf16((float)s);
+    }
+  }
+
+  // Last workgroup to finish: top-k over all logits.
+  __threadfence();
+  __syncthreads();
+  if (t == 0) is_last = atomicAdd(a.ctr, 1) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+  for (int e = t; e < kE; e += 256) lgs[e] = ld_coherent(a.logits + e);
+  __syncthreads();
+  if (wave == 0) {
+    topk_wave(lgs, kE, kTopK, lane, sid, swt);
+    if (lane == 0) {
+      int ids[kTopK];
+      float w[kTopK];
+      for (int i = 0; i < kTopK; ++i) {
+        ids[i] = (int)sid[i];
+        w[i] = bf16_bits_to_f32(swt[i]);
+        a.ids[i] = sid[i];
+        a.wts[i] = swt[i];
+        if (a.ids_out) a.ids_out[i] = ids[i];
+        if (a.wts_out) a.wts_out[i] = swt[i];
+      }
+      for (int i = 1; i < kTopK; ++i) {  // ascending expert id (combine order)
+        const int ki = ids[i];
+        const float wi = w[i];
+        int m = i - 1;
+        while (m >= 0 && ids[m] > ki) {
+          ids[m + 1] = ids[m];
+          w[m + 1] = w[m];
+          --m;
+        }
+        ids[m + 1] = ki;
+        w[m + 1] = wi;
+      }
+      for (int i = 0; i < kTopK; ++i) {
+        a.sel[i] = ids[i];
+        a.selw[i] = w[i];
+      }
+      __hip_atomic_store(a.ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// gate_up of slot blockIdx.y (0..7 routed W8A8, 8 = shared W8A16), 8 output
+// columns per block: rows n0..n0+7 (gate) and kI+n0.. (up), K = kH.
+constexpr int kGuPairs = 8;
+__global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
+  constexpr int G = kH / 128;
+  constexpr int R = 2 * kGuPairs;
+  __shared__ __align__(16) unsigned char xbuf[kH * 2];
+  __shared__ float xs[G];
+  __shared__ float ws[R * G];
+  __shared__ float partf[R * G];
+  __shared__ int parti[R * G];
+  const int slot = blockIdx.y;
+  const bool shared = slot == kTopK;
+  const int n0 = blockIdx.x * kGuPairs;
+  const int e = shared ? kE : a.sel[slot];
+  const int8_t *wq = a.gu_q + (int64_t)e * a.gu_qes;
+  const float *wsrc = a.gu_s + (int64_t)e * a.gu_ses;
+  const RowMap map{n0, kI + n0, kGuPairs};
+  RowLoads<8> L;
+  L.issue(R, G, [&](int r) { return wq + (int64_t)map(r) * kH; });
+
+  const int t = threadIdx.x;
+  if (shared) {
+    for (int i = t; i < kH / 8; i += 256)
+      reinterpret_cast<u32x4 *>(xbuf)[i] = ldg16(a.xn + i * 8);
+  } else {
+    for (int i = t; i < kH / 16; i += 256)
+      reinterpret_cast<u32x4 *>(xbuf)[i] = ldg16(a.xq + i * 16);
+    if (t < G) xs[t] = a.xs[t];
+  }
+  for (int i = t; i < R * G; i += 256) ws[i] = wsrc[(int64_t)map(i / G) * G + (i % G)];
+  __syncthreads();
+
+  const int sub = t & 7;
+  if (shared) {
+    const uint16_t *x16 = reinterpret_cast<const uint16_t *>(xbuf);
+    L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
+      uint32_t wd[8];
+      dequant16<BF16>(w, ok ? ws[f] : 0.0f, wd);
+      const uint16_t *xp = x16 + g * 128 + sub * 16;
+      const float p = octet_sum_f32(dot16_w16<BF16>(wd, *reinterpret_cast<const u32x4 *>(xp),
+                                                    *reinterpret_cast<const u32x4 *>(xp + 8)));
+      if (ok && sub == 0) partf[f] = p;
+    });
+  } else {
+    const int8_t *x8 = reinterpret_cast<const int8_t *>(xbuf);
+    L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
+      const int p = octet_sum_i32(
+          dot16_i8(w, *reinterpret_cast<const u32x4 *>(x8 + g * 128 + sub * 16)));
+      if (ok && sub == 0) parti[f] = p;
+    });
+  }
+  __syncthreads();
+  if (t < kGuPairs) {
+    float gate, up;
+    if (shared) {
+      float sg = 0.0f, su = 0.0f;
+      for (int g = 0; g < G; ++g) {
+        sg += partf[t * G + g];
+        su += partf[(kGuPairs + t) * G + g];
+      }
+      gate = round_bf16(sg);
+      up = round_bf16(su);
+    } else {
+      gate = round_bf16(w8a8_epilogue(parti + t * G, xs, ws + t * G, G));
+      up = round_bf16(w8a8_epilogue(parti + (kGuPairs + t) * G, xs, ws + (kGuPairs + t) * G, G));
+    }
+    a.hbuf[slot * kI + n0 + t] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
+  }
+}
+
+// down rows of all 9 slots for 8 output columns, combine, gated shared add,
+// residual add.
+constexpr int kDnCols = 8;
+__global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
+  constexpr int G = kI / 128;
+  constexpr int R = (kTopK + 1) * kDnCols;
+  __shared__ __align__(16) int8_t xq[kTopK * kI];
+  __shared__ float xs[kTopK * G];
+  __shared__ __align__(16) uint16_t xsh[kI];
+  __shared__ float ws[R * G];
+  __shared__ int parti[kTopK * kDnCols * G];
+  __shared__ float partf[kDnCols * G];
+  const int t = threadIdx.x;
+  const int c0 = blockIdx.x * kDnCols;
+  int ex[kTopK + 1];
+#pragma unroll
+  for (int s = 0; s < kTopK; ++s) ex[s] = a.sel[s];
+  ex[kTopK] = kE;
+  auto rowp = [&](int r) {
+    const int s = r / kDnCols;
+    int e = kE;
+#pragma unroll
+    for (int j = 0; j < kTopK; ++j)
+      if (s == j) e = ex[j];
+    return a.dn_q + (int64_t)e * a.dn_qes + (int64_t)(c0 + r % kDnCols) * kI;
+  };
+  RowLoads<12> L;
+  L.issue(R, G, rowp);
+
+  // Row-quantize the 8 routed SwiGLU outputs (w8a8.quantize on [8, kI]).
+  quantize_rows_to_lds<BF16>(a.hbuf, kI, kTopK, kI, xq, xs);
+  for (int i = t; i < kI / 8; i += 256)
+    reinterpret_cast<u32x4 *>(xsh)[i] = ldg16(a.hbuf + kTopK * kI + i * 8);
+  for (int i = t; i < R * G; i += 256) {
+    const int r = i / G, g = i % G;
+    const int s = r / kDnCols;
+    const int e = s < kTopK ? a.sel[s] : kE;
+    ws[i] = a.dn_s[(int64_t)e * a.dn_ses + (int64_t)(c0 + r % kDnCols) * G + g];
+  }
+  __syncthreads();
+
+  const int sub = t & 7;
+  L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
+    const int s = r / kDnCols;  // uniform across the wave instruction
+    if (s < kTopK) {
+      const int p = octet_sum_i32(
+          dot16_i8(w, *reinterpret_cast<const u32x4 *>(xq + s * kI + g * 128 + sub * 16)));
+      if (ok && sub == 0) parti[f] = p;
+    } else {
+      uint32_t wd[8];
+      dequant16<BF16>(w, ok ? ws[f] : 0.0f, wd);
+      const uint16_t *xp = xsh + g * 128 + sub * 16;
+      const float p = octet_sum_f32(dot16_w16<BF16>(wd, *reinterpret_cast<const u32x4 *>(xp),
+                                                    *reinterpret_cast<const u32x4 *>(xp + 8)));
+      if (ok && sub == 0) partf[f - kTopK * kDnCols * G] = p;
+    }
+  });
+  __syncthreads();
+  if (t < kDnCols) {
+    float acc = 0.0f;
+    for (int s = 0; s < kTopK; ++s) {
+      const int r = s * kDnCols + t;
+      const float v = round_bf16(w8a8_epilogue(parti + r * G, xs + s * G, ws + r * G, G));
+      acc = round_bf16(acc + round_bf16(v * a.selw[s]));
+    }
+    float vs = 0.0f;
+    for (int g = 0; g < G; ++g) vs += partf[t * G + g];
+    const float vsh = round_bf16(vs);
+    const float sig = round_bf16(sigmoid_f32(a.gl[0]));
+    const float out = round_bf16(acc + round_bf16(sig * vsh));
+    const int n = c0 + t;
+    a.h[n] = f32_to_bf16_bits(bf16_bits_to_f32(a.h[n]) + out);
+  }
+}
+
+// ------------------------------------------------------------------ prefill
+// RMSNorm of each token row + the shared-expert gate logit (fp64 dot).
+__global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a) {
+  __shared__ float xf[kH];
+  __shared__ float red[4];
+  __shared__ double dred[4];
+  const int tok = blockIdx.x;
+  const int t = threadIdx.x;
+  norm_row_to_lds(a.h + (int64_t)tok * kH, a.norm_w, a.eps, xf, red);
+  constexpr int PER = kH / 256;
+  u32x4 packed;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    packed[j] = BF16::pack2(xf[t * PER + 2 * j], xf[t * PER + 2 * j + 1]);
+  *reinterpret_cast<u32x4 *>(a.xn + (int64_t)tok * kH + t * PER) = packed;
+  const u32x4 gv = ldg16(a.gate_w + t * PER);
+  double acc = 0.0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    acc = __builtin_fma((double)xf[t * PER + 2 * j], (double)bf16_bits_to_f32(gv[j] & 0xFFFFu), acc);
+    acc = __builtin_fma((double)xf[t * PER + 2 * j + 1], (double)bf16_bits_to_f32(gv[j] >> 16), acc);
+  }
+  acc = wave_sum_f64(acc);
+  if ((t & 63) == 0) dred[t >> 6] = acc;
+  __syncthreads();
+  if (t == 0) a.gl[tok] = round_bf16((float)(dred[0] + dred[1] + dred[2] + dred[3]));
+}
+
+// Per token: routed combine in ascending expert order, gated shared add,
+// residual add (in place on h).  256 threads x 8 columns.
+__global__ __launch_bounds__(256) void prefill_combine_kernel(LayerArgs a, const int64_t *ordered,
+                                                              const int64_t *slots,
+                                                              const uint16_t *vbuf, int64_t R) {
+  const int tok = blockIdx.x;
+  const int c = threadIdx.x * 8;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < kTopK; ++i) {
+    const int64_t route = ordered[(int64_t)tok * kTopK + i];
+    const int64_t slot = slots[(int64_t)tok * kTopK + i];
+    const float w = bf16_bits_to_f32(a.wts[(int64_t)tok * kTopK + slot]);
+    const u32x4 v = ldg16(vbuf + route * kH + c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[2 * j] = round_bf16(acc[2 * j] + round_bf16(bf16_bits_to_f32(v[j] & 0xFFFFu) * w));
+      acc[2 * j + 1] = round_bf16(acc[2 * j + 1] + round_bf16(bf16_bits_to_f32(v[j] >> 16) * w));
+    }
+  }
+  const float sig = round_bf16(sigmoid_f32(a.gl[tok]));
+  const u32x4 sv = ldg16(vbuf + (R + tok) * kH + c);
+  uint16_t *hp = a.h + (int64_t)tok * kH + c;
+  const u32x4 hv = ldg16(hp);
+  u32x4 outv;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float o0 = round_bf16(acc[2 * j] + round_bf16(sig * bf16_bits_to_f32(sv[j] & 0xFFFFu)));
+    float o1 = round_bf16(acc[2 * j + 1] + round_bf16(sig * bf16_bits_to_f32(sv[j] >> 16)));
+    o0 = bf16_bits_to_f32(hv[j] & 0xFFFFu) + o0;
+    o1 = bf16_bits_to_f32(hv[j] >> 16) + o1;
+    outv[j] = BF16::pack2(o0, o1);
+  }
+  *reinterpret_cast<u32x4 *>(hp) = outv;
+}
+
+__global__ void export_routing_kernel(const int64_t *ids, const uint16_t *wts, int32_t *ids_out,
+                                      uint16_t *wts_out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  if (ids_out) ids_out[i] = (int32_t)ids[i];
+  if (wts_out) wts_out[i] = wts[i];
+}
+
+__global__ void fill_zero_kernel(uint32_t *p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+}  // namespace lm
+
+using namespace lm;
+
+extern "C" int64_t lm_moe_workspace_bytes(int64_t max_tokens, int64_t hidden, int64_t inter,
+                                          int64_t experts, int64_t top_k) {
+  if (hidden != kH || inter != kI || experts != kE || top_k != kTopK || max_tokens < 1) return -1;
+  return layout(max_tokens).total;
+}
+
+extern "C" int lm_moe_workspace_init(void *workspace, int64_t bytes, void *stream) {
+  LM_REQUIRE(workspace && bytes >= 256, LM_EINVAL, "workspace too small");
+  fill_zero_kernel<<<1, 256, 0, as_stream(stream)>>>(static_cast<uint32_t *>(workspace), 64);
+  return check_launch("fill_zero_kernel");
+}
+
+extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t tokens,
+                                    int64_t hidden, int64_t inter, int64_t experts, int64_t top_k,
+                                    float eps, void *workspace, int64_t workspace_bytes,
+                                    int32_t *ids_out, void *weights_out,
+                                    void *const *phase_events, void *stream) {
+  LM_REQUIRE(hidden == kH && inter == kI && experts == kE && top_k == kTopK, LM_EINVAL,
+             "fused MoE layer supports hidden 2048, intermediate 512, 256 experts, top-8");
+  LM_REQUIRE(tokens >= 1 && tokens <= 65536, LM_EINVAL, "invalid token count");
+  LM_REQUIRE(layer && h && workspace, LM_EINVAL, "null pointer");
+  LM_REQUIRE(layer->router_w && layer->shared_gate_w && layer->gu_q && layer->gu_s &&
+                 layer->dn_q && layer->dn_s,
+             LM_EINVAL, "null layer weight");
+  const WsLayout w = layout(tokens);
+  LM_REQUIRE(workspace_bytes >= w.total, LM_ENOMEM, "workspace too small for this token count");
+  unsigned char *ws = static_cast<unsigned char *>(workspace);
+  LayerArgs a{};
+  a.router_w = static_cast<const uint16_t *>(layer->router_w);
+  a.router_bias = layer->router_bias;
+  a.gate_w = static_cast<const uint16_t *>(layer->shared_gate_w);
+  a.norm_w = layer->norm_w;
+  a.gu_q = layer->gu_q;
+  a.gu_s = layer->gu_s;
+  a.dn_q = layer->dn_q;
+  a.dn_s = layer->dn_s;
+  a.gu_qes = layer->gu_q_expert_stride;
+  a.gu_ses = layer->gu_s_expert_stride;
+  a.dn_qes = layer->dn_q_expert_stride;
+  a.dn_ses = layer->dn_s_expert_stride;
+  a.h = static_cast<uint16_t *>(h);
+  a.eps = eps;
+  a.ctr = reinterpret_cast<int *>(ws + w.ctr);
+  a.xn = reinterpret_cast<uint16_t *>(ws + w.xn);
+  a.gl = reinterpret_cast<float *>(ws + w.gl);
+  a.logits = reinterpret_cast<float *>(ws + w.logits);
+  a.ids = reinterpret_cast<int64_t *>(ws + w.ids);
+  a.wts = reinterpret_cast<uint16_t *>(ws + w.wts);
+  a.sel = reinterpret_cast<int *>(ws + w.sel);
+  a.selw = reinterpret_cast<float *>(ws + w.selw);
+  a.xq = reinterpret_cast<int8_t *>(ws + w.xq);
+  a.xs = reinterpret_cast<float *>(ws + w.xs);
+  a.hbuf = reinterpret_cast<uint16_t *>(ws + w.hbuf);
+  a.ids_out = ids_out;
+  a.wts_out = static_cast<uint16_t *>(weights_out);
+  hipStream_t st = as_stream(stream);
+  auto mark = [&](int i) -> int {
+    if (!phase_events) return LM_OK;
+    hipError_t e = hipEventRecord(static_cast<hipEvent_t>(phase_events[i]), st);
+    return e == hipSuccess ? LM_OK : set_error(LM_ELAUNCH, "hipEventRecord failed");
+  };
+
+  if (tokens == 1) {
+    if (int rc = mark(0)) return rc;
+    decode_router_kernel<<<kE / 4 + 1, 256, 0, st>>>(a);
+    if (int rc = check_launch("decode_router_kernel")) return rc;
+    if (int rc = mark(1)) return rc;
+    decode_gate_up_kernel<<<dim3(kI / kGuPairs, kTopK + 1), 256, 0, st>>>(a);
+    if (int rc = check_launch("decode_gate_up_kernel")) return rc;
+    if (int rc = mark(2)) return rc;
+    decode_down_kernel<<<kH / kDnCols, 256, 0, st>>>(a);
+    if (int rc = check_launch("decode_down_kernel")) return rc;
+    return mark(3);
+  }
+
+  const int64_t T = tokens, R = T * kTopK;
+  int64_t *pos = reinterpret_cast<int64_t *>(ws + w.pos);
+  int64_t *table = reinterpret_cast<int64_t *>(ws + w.table);
+  int64_t *ordered = reinterpret_cast<int64_t *>(ws + w.ordered);
+  int64_t *slots = reinterpret_cast<int64_t *>(ws + w.slots);
+  uint16_t *vbuf = reinterpret_cast<uint16_t *>(ws + w.vbuf);
+  if (int rc = mark(0)) return rc;
+  prefill_norm_gate_kernel<<<(unsigned)T, 256, 0, st>>>(a);
+  if (int rc = check_launch("prefill_norm_gate_kernel")) return rc;
+  if (int rc = mark(1)) return rc;
+  if (int rc = router_logits(a.xn, a.router_w, a.router_bias, a.logits, T, kE, kH, st)) return rc;
+  if (int rc = mark(2)) return rc;
+  if (int rc = router_topk(a.logits, T, kE, kTopK, a.ids, a.wts, st)) return rc;
+  if (int rc = mark(3)) return rc;
+  if (int rc = route_plan(a.ids, T, kTopK, kE, kBM, pos, table, w.max_tiles, ordered, slots, T, st))
+    return rc;
+  if (int rc = mark(4)) return rc;
+  if (int rc = routed_gemm(a.xn, a.gu_q, a.gu_s, pos, table, w.n_tiles, kBM, a.hbuf, 2 * kI, kH,
+                           true, true, a.gu_qes, a.gu_ses, kH, st))
+    return rc;
+  if (int rc = mark(5)) return rc;
+  if (int rc = routed_gemm(a.hbuf, a.dn_q, a.dn_s, pos, table, w.n_tiles, kBM, vbuf, kH, kI, false,
+                           false, a.dn_qes, a.dn_ses, kI, st))
+    return rc;
+  if (int rc = mark(6)) return rc;
+  prefill_combine_kernel<<<(unsigned)T, 256, 0, st>>>(a, ordered, slots, vbuf, R);
+  if (int rc = check_launch("prefill_combine_kernel")) return rc;
+  if (int rc = mark(7)) return rc;
+  if (ids_out || weights_out) {
+    export_routing_kernel<<<cdiv(R, 256), 256, 0, st>>>(a.ids, a.wts, ids_out, a.wts_out, R);
+    return check_launch("export_routing_kernel");
+  }
+  return LM_OK;
+}

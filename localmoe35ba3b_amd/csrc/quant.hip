@@ -1,0 +1,114 @@
+// Group-128 int8 quantizers.
+//
+//  * lm_quantize_weight_g128: the offline weight format producer
+//    (convert.py:31-37): s = max(amax / 127, 1e-30), q = clamp(rne(w / s), +-127).
+//  * lm_act_quant_g128: dynamic per-row activation quantization of the W8A8
+//    decode path (w8a8.py:8-22): s = max(amax, 1e-10) * fl32(1/127),
+//    q = rint(x / s) with IEEE division (|x / s| <= 127 by construction).
+//
+// One 128-element group is handled by 32 lanes holding 4 elements each, so a
+// wave quantizes two groups per iteration with fully coalesced 16-byte loads.
+#include "common.hpp"
+
+namespace lm {
+
+__global__ __launch_bounds__(256) void quantize_weight_kernel(const float *__restrict__ w,
+                                                              int8_t *__restrict__ q,
+                                                              float *__restrict__ s,
+                                                              int64_t ngroups) {
+  const int lane = threadIdx.x & 63;
+  const int l = lane & 31;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t g2 = wave; g2 * 2 < ngroups; g2 += nwaves) {
+    const int64_t grp = g2 * 2 + (lane >> 5);
+    const bool valid = grp < ngroups;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (valid) v = *reinterpret_cast<const f32x4 *>(w + grp * 128 + l * 4);
+    float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+    const float sc = fmaxf(a / 127.0f, 1e-30f);
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float r = rintf(v[i] / sc);
+      r = fminf(fmaxf(r, -127.0f), 127.0f);
+      packed |= ((uint32_t)(uint8_t)(int8_t)(int)r) << (8 * i);
+    }
+    if (valid) {
+      *reinterpret_cast<uint32_t *>(q + grp * 128 + l * 4) = packed;
+      if (l == 0) s[grp] = sc;
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t *__restrict__ x,
+                                                        int8_t *__restrict__ q,
+                                                        float *__restrict__ s,
+                                                        int64_t ngroups) {
+  const int lane = threadIdx.x & 63;
+  const int l = lane & 31;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const float inv127 = (float)(1.0 / 127.0);
+  for (int64_t g2 = wave; g2 * 2 < ngroups; g2 += nwaves) {
+    const int64_t grp = g2 * 2 + (lane >> 5);
+    const bool valid = grp < ngroups;
+    uint2 raw = make_uint2(0, 0);
+    if (valid) raw = *reinterpret_cast<const uint2 *>(x + grp * 128 + l * 4);
+    float v[4] = {T::to_f32(raw.x & 0xFFFFu), T::to_f32(raw.x >> 16), T::to_f32(raw.y & 0xFFFFu),
+                  T::to_f32(raw.y >> 16)};
+    float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+    const float sc = fmaxf(a, 1e-10f) * inv127;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[i] / sc)) << (8 * i);
+    if (valid) {
+      *reinterpret_cast<uint32_t *>(q + grp * 128 + l * 4) = packed;
+      if (l == 0) s[grp] = sc;
+    }
+  }
+}
+
+static unsigned quant_grid(int64_t ngroups) {
+  int64_t waves = (ngroups + 1) / 2;
+  int64_t blocks = (waves + 3) / 4;
+  if (blocks > 4096) blocks = 4096;
+  return (unsigned)(blocks < 1 ? 1 : blocks);
+}
+
+}  // namespace lm
+
+using namespace lm;
+
+extern "C" int lm_quantize_weight_g128(const float *w, int8_t *q, float *s, int64_t rows,
+                                       int64_t k, void *stream) {
+  LM_REQUIRE(rows >= 0 && k > 0 && k % 128 == 0, LM_EINVAL, "Invalid INT8 group geometry");
+  LM_REQUIRE(rows == 0 || (w && q && s), LM_EINVAL, "null pointer");
+  const int64_t ngroups = rows * (k / 128);
+  if (ngroups == 0) return LM_OK;
+  quantize_weight_kernel<<<quant_grid(ngroups), 256, 0, as_stream(stream)>>>(w, q, s, ngroups);
+  return check_launch("quantize_weight_kernel");
+}
+
+extern "C" int lm_act_quant_g128(const void *x, int x_dtype, int8_t *q, float *s, int64_t rows,
+                                 int64_t k, void *stream) {
+  LM_REQUIRE(rows >= 0 && k > 0 && k % 128 == 0, LM_EINVAL,
+             "Expected CUDA rows with K divisible by 128");
+  LM_REQUIRE(x_dtype == LM_BF16 || x_dtype == LM_FP16, LM_EINVAL,
+             "Expected CUDA rows with K divisible by 128");
+  LM_REQUIRE(rows == 0 || (x && q && s), LM_EINVAL, "null pointer");
+  const int64_t ngroups = rows * (k / 128);
+  if (ngroups == 0) return LM_OK;
+  const uint16_t *xp = static_cast<const uint16_t *>(x);
+  if (x_dtype == LM_BF16)
+    act_quant_kernel<BF16><<<quant_grid(ngroups), 256, 0, as_stream(stream)>>>(xp, q, s, ngroups);
+  else
+    act_quant_kernel<FP16><<<quant_grid(ngroups), 256, 0, as_stream(stream)>>>(xp, q, s, ngroups);
+  return check_launch("act_quant_kernel");
+}

@@ -1,0 +1,172 @@
+"""HBM-resident synthetic MoE-FFN stack (40 x [RMSNorm -> MoE block -> residual]).
+
+Replaces the reference's CPU-pinned expert bank, 7 GiB slab arena and
+frequency-retention cache (runtime/prefill.py:88-164, runtime/slab_cache.py,
+runtime/frequency_seed.py): on a 288 GB MI355X the whole int8 bank of every
+layer is resident in HBM, so prefill reads each active expert straight from
+HBM and decode needs no cache, no host routing read and no H2D copy.
+
+Bank layout, per stack (all contiguous, expert-major like the reference's
+converted artifact, convert.py:96-97):
+  gu_q  int8 [L, E+1, 2I, H]   gu_s fp32 [L, E+1, 2I, H/128]
+  dn_q  int8 [L, E+1, H, I]    dn_s fp32 [L, E+1, H, I/128]
+expert index E is the always-on shared expert (its gate_proj / up_proj rows
+concatenated, exact because scales are per row).  Router weights bf16
+[L, E, H], shared-expert gate bf16 [L, H]; the RMSNorm weight is zero
+(scale 1 + w = 1), as for a freshly initialised Qwen3_5MoeRMSNorm.
+
+Weights are drawn on the GPU from per-(layer, matrix) seeds, N(0, 0.02) fp32,
+and quantized by the group-128 HIP quantizer.
+"""
+import ctypes
+import math
+
+import numpy as np
+import torch
+
+from .. import _lib
+from ..convert import quantize_g128
+
+HIDDEN, INTER, EXPERTS, TOP_K = 2048, 512, 256, 8
+EPS = 1e-6
+
+
+def matrix_seed(base, layer, matrix, chunk=0):
+    """Seed of one generated weight block: matrix 0 router, 1 shared gate,
+    2 gate_up, 3 down; chunk = expert block index."""
+    return (base * 1_000_003 + layer * 10_007 + matrix * 101 + chunk) % (2 ** 63)
+
+
+def zipf_bias(experts=EXPERTS, s=1.1, seed=3):
+    """Per-expert router-logit offset that skews popularity like Zipf(s):
+    offset_e = ln(r_e^-s / sum_j j^-s) - mean_e(...), r = seeded permutation of
+    the ranks 1..E (numpy default_rng(seed).permutation).  fp64 -> fp32 once."""
+    ranks = np.random.default_rng(seed).permutation(experts) + 1
+    logp = -s * np.log(ranks.astype(np.float64)) - math.log(
+        np.sum(np.arange(1, experts + 1, dtype=np.float64) ** -s))
+    return (logp - logp.mean()).astype(np.float32)
+
+
+class SyntheticMoEStack:
+    """Random-init 35B-A3B-class MoE-FFN stack resident in HBM.
+
+    layers/experts may be reduced for tests; the fused layer kernels require
+    hidden 2048, intermediate 512, 256 experts and top-8.
+    """
+
+    def __init__(self, layers=40, seed=4, device='cuda', max_tokens=2048, router_bias=None,
+                 chunk_experts=32):
+        self.L = layers
+        self.E, self.H, self.I, self.K = EXPERTS, HIDDEN, INTER, TOP_K
+        self.device = torch.device(device)
+        self.max_tokens = max_tokens
+        dev = self.device
+        E1 = self.E + 1
+        self.gu_q = torch.empty((layers, E1, 2 * self.I, self.H), dtype=torch.int8, device=dev)
+        self.gu_s = torch.empty((layers, E1, 2 * self.I, self.H // 128), dtype=torch.float32,
+                                device=dev)
+        self.dn_q = torch.empty((layers, E1, self.H, self.I), dtype=torch.int8, device=dev)
+        self.dn_s = torch.empty((layers, E1, self.H, self.I // 128), dtype=torch.float32,
+                                device=dev)
+        self.router_w = torch.empty((layers, self.E, self.H), dtype=torch.bfloat16, device=dev)
+        self.gate_w = torch.empty((layers, self.H), dtype=torch.bfloat16, device=dev)
+        self.router_bias = None
+        if router_bias is not None:
+            self.router_bias = torch.as_tensor(router_bias, dtype=torch.float32).to(dev)
+        gen = torch.Generator(device=dev)
+        for l in range(layers):
+            gen.manual_seed(matrix_seed(seed, l, 0))
+            self.router_w[l] = (torch.randn((self.E, self.H), generator=gen, device=dev)
+                                * 0.02).to(torch.bfloat16)
+            gen.manual_seed(matrix_seed(seed, l, 1))
+            self.gate_w[l] = (torch.randn(self.H, generator=gen, device=dev) * 0.02).to(
+                torch.bfloat16)
+            for c0 in range(0, E1, chunk_experts):
+                c1 = min(E1, c0 + chunk_experts)
+                gen.manual_seed(matrix_seed(seed, l, 2, c0 // chunk_experts))
+                w = torch.randn((c1 - c0, 2 * self.I, self.H), generator=gen, device=dev) * 0.02
+                self.gu_q[l, c0:c1], self.gu_s[l, c0:c1] = quantize_g128(w)
+                gen.manual_seed(matrix_seed(seed, l, 3, c0 // chunk_experts))
+                w = torch.randn((c1 - c0, self.H, self.I), generator=gen, device=dev) * 0.02
+                self.dn_q[l, c0:c1], self.dn_s[l, c0:c1] = quantize_g128(w)
+                del w
+        nbytes = _lib.lib().lm_moe_workspace_bytes(max_tokens, self.H, self.I, self.E, self.K)
+        if nbytes < 0:
+            raise ValueError('unsupported MoE geometry')
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _lib.call('lm_moe_workspace_init', self.workspace.data_ptr(), nbytes, _lib.stream(dev))
+        self._structs = [self._layer_struct(l) for l in range(layers)]
+
+    # ------------------------------------------------------------------ views
+    def bank_bytes(self):
+        return sum(t.numel() * t.element_size() for t in
+                   (self.gu_q, self.gu_s, self.dn_q, self.dn_s, self.router_w, self.gate_w))
+
+    def _layer_struct(self, l):
+        s = _lib.MoeLayer()
+        s.router_w = self.router_w[l].data_ptr()
+        s.router_bias = self.router_bias.data_ptr() if self.router_bias is not None else None
+        s.shared_gate_w = self.gate_w[l].data_ptr()
+        s.norm_w = None
+        s.gu_q = self.gu_q[l].data_ptr()
+        s.gu_s = self.gu_s[l].data_ptr()
+        s.dn_q = self.dn_q[l].data_ptr()
+        s.dn_s = self.dn_s[l].data_ptr()
+        s.gu_q_expert_stride = self.gu_q.stride(1)
+        s.gu_s_expert_stride = self.gu_s.stride(1)
+        s.dn_q_expert_stride = self.dn_q.stride(1)
+        s.dn_s_expert_stride = self.dn_s.stride(1)
+        return s
+
+    def banks(self, l):
+        """Routed-expert banks of layer l in the reference routed_moe format."""
+        return [self.gu_q[l, :self.E], self.gu_s[l, :self.E], self.dn_q[l, :self.E],
+                self.dn_s[l, :self.E]]
+
+    # ------------------------------------------------------------------ forward
+    def layer_forward(self, h, l, ids_out=None, weights_out=None, events=None):
+        """h bf16 [T, H] updated in place: h = h + block(rmsnorm(h))."""
+        if h.dtype != torch.bfloat16 or not h.is_contiguous() or h.shape[-1] != self.H:
+            raise ValueError('expected contiguous bf16 [tokens, 2048] hidden states')
+        tokens = h.shape[0]
+        if tokens > self.max_tokens:
+            raise MemoryError('token count exceeds the workspace of this stack')
+        ev = None
+        if events is not None:
+            ev = (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
+        _lib.call('lm_moe_layer_forward', ctypes.byref(self._structs[l]), h.data_ptr(), tokens,
+                  self.H, self.I, self.E, self.K, EPS, self.workspace.data_ptr(),
+                  self.workspace.numel(), _lib.ptr(ids_out), _lib.ptr(weights_out), ev,
+                  _lib.stream(h.device))
+        return h
+
+    def forward(self, h, layers=None):
+        for l in range(self.L if layers is None else layers):
+            self.layer_forward(h, l)
+        return h
+
+    def prefill(self, x, chunk=2048):
+        """Runs all layers over x [T, H] in chunks of `chunk` tokens; returns h."""
+        out = x.clone()
+        for c0 in range(0, x.shape[0], chunk):
+            self.forward(out[c0:c0 + chunk])
+        return out
+
+    # ------------------------------------------------------------------ oracle views
+    def layer_host(self, l, experts=None):
+        """Host (numpy) copy of layer l for the CPU oracle.  With `experts`
+        only those routed experts (plus the shared expert E) are copied and the
+        bank entries are dicts keyed by expert id."""
+        E = self.E
+        names = ('gu_q', 'gu_s', 'dn_q', 'dn_s')
+        src = (self.gu_q, self.gu_s, self.dn_q, self.dn_s)
+        if experts is None:
+            banks = {n: t[l].cpu().numpy() for n, t in zip(names, src)}
+        else:
+            sel = sorted(set(int(e) for e in experts) | {E})
+            banks = {n: {e: t[l, e].cpu().numpy() for e in sel} for n, t in zip(names, src)}
+        return dict(router_w=self.router_w[l].float().cpu().numpy(),
+                    router_bias=None if self.router_bias is None
+                    else self.router_bias.cpu().numpy(),
+                    shared_gate_w=self.gate_w[l].float().cpu().numpy(),
+                    norm_w=None, **banks)

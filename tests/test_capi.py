@@ -1,0 +1,86 @@
+"""CPU checks of the C ABI: the library loads, exports every declared symbol,
+validates arguments before any launch, and the host route planner matches the
+oracle.  No kernel is launched here (there may be no GPU)."""
+import ctypes
+import pathlib
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from localmoe35ba3b_amd import _lib
+from localmoe35ba3b_amd.operators import int8, routing, w8a8
+from localmoe35ba3b_amd.runtime import gpu_routes
+from oracle import moe_oracle as O
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / 'include' / 'localmoe35ba3b.h'
+
+
+def declared_functions():
+    text = re.sub(r'/\*.*?\*/', '', HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r'\b(lm_[a-z0-9_]+)\s*\(', text)))
+
+
+def test_header_declares_what_python_binds():
+    names = declared_functions()
+    assert len(names) >= 20
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert b'gfx950' in lib.lm_version()
+
+
+def test_invalid_geometry_rejected_before_launch():
+    lib = _lib.lib()
+    rc = lib.lm_w8a16_linear(None, None, None, None, 4, 64, 100, 0, 0, None)
+    assert rc == _lib.LM_EINVAL
+    assert b'Invalid INT8 group geometry' in lib.lm_last_error()
+    assert lib.lm_w8a16_linear(None, None, None, None, 4, 64, 128, 7, 0, None) == _lib.LM_EINVAL
+    assert b'FP16/BF16' in lib.lm_last_error()
+    assert lib.lm_act_quant_g128(None, 0, None, None, 2, 130, None) == _lib.LM_EINVAL
+    assert b'K divisible by 128' in lib.lm_last_error()
+    assert lib.lm_route_plan(None, 4, 8, 300, 16, None, None, 0, None, None, None) == _lib.LM_EINVAL
+    assert lib.lm_route_plan(None, 4, 8, 256, 16, None, None, 5, None, None, None) == _lib.LM_EINVAL
+    assert lib.lm_routed_gemm_w8a16(None, None, None, None, None, 1, 200, None, 64, 128, 1, 0, 0,
+                                    None) == _lib.LM_EINVAL
+    assert lib.lm_router_topk(None, None, None, None, None, None, 1, 512, 2048, 8,
+                              None) == _lib.LM_EINVAL
+    assert lib.lm_w8a8_linear(None, None, None, None, 9, 64, 128, 0, None) == _lib.LM_EINVAL
+
+
+def test_status_maps_to_reference_exceptions():
+    with pytest.raises(ValueError, match='Invalid INT8 group geometry'):
+        _lib.call('lm_w8a16_linear', None, None, None, None, 1, 8, 100, 0, 0, None)
+
+
+def test_python_wrappers_validate_like_reference():
+    x = torch.zeros(2, 256, dtype=torch.bfloat16)
+    q = torch.zeros(64, 256, dtype=torch.int8)
+    s = torch.zeros(64, 2)
+    with pytest.raises(ValueError, match='W8A16 requires CUDA FP16/BF16 activations'):
+        int8.linear(x, q, s)
+    with pytest.raises(ValueError, match='Expected CUDA rows with K divisible by 128'):
+        w8a8.quantize(x)
+    with pytest.raises(ValueError, match='Expected contiguous CUDA'):
+        gpu_routes.plan(torch.zeros(2, 8, dtype=torch.int64), 256, 16)
+    with pytest.raises(ValueError, match='Expected nonempty CPU'):
+        routing.plan_routes(torch.zeros(0, 8, dtype=torch.int64), 256)
+    with pytest.raises(ValueError, match='Out-of-range expert ID'):
+        routing.plan_routes(torch.tensor([[0, 256]]), 256)
+    with pytest.raises(ValueError, match='Out-of-range expert ID'):
+        routing.plan_routes(torch.tensor([[-1, 3]]), 256)
+
+
+@pytest.mark.parametrize('t,k,e', [(1, 8, 256), (13, 8, 256), (2048, 8, 256), (5, 3, 7)])
+def test_host_plan_routes_matches_oracle(t, k, e):
+    rng = np.random.default_rng(t + e)
+    ids = np.stack([rng.choice(e, size=k, replace=False) for _ in range(t)]).astype(np.int64)
+    positions, segments = routing.plan_routes(torch.from_numpy(ids), e)
+    ref_pos, ref_seg = O.plan_routes(ids, e)
+    assert np.array_equal(positions.numpy(), ref_pos)
+    assert segments == ref_seg
