@@ -105,10 +105,12 @@ __global__ __launch_bounds__(256) void router_logits_mfma(const uint16_t *__rest
       bv1 = bn1;
     }
   }
-  // D layout: lane holds column (lane & 15), rows 4 * (lane >> 4) + i.
+  // D layout of the f64 16x16x4 MFMA: lane holds column (lane & 15) and
+  // rows (lane >> 4) + 4 i, i = 0..3 (unlike the 4 (lane >> 4) + i rows of the
+  // 32-bit-output 16x16 MFMAs).
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int t = t0 + q * 4 + i;
+    const int t = t0 + q + 4 * i;
     if (t >= T) continue;
     const int ea = e0 + r, eb = e0 + 16 + r;
     if (ea < E) {
