@@ -13,6 +13,7 @@ import sys
 
 CSRC = pathlib.Path(__file__).resolve().parent
 PKG = CSRC.parent
+INCLUDE = PKG.parent / 'include'
 LIB = PKG / 'liblocalmoe35ba3b.so'
 SOURCES = sorted(CSRC.glob('*.hip'))
 ARCH = os.environ.get('LM_OFFLOAD_ARCH', 'gfx950')
@@ -33,7 +34,7 @@ def hipcc():
 
 
 def _compile(src, obj):
-    cmd = [hipcc(), *COMMON, '-c', str(src), '-o', str(obj)]
+    cmd = [hipcc(), *COMMON, '-I', str(INCLUDE), '-c', str(src), '-o', str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "'-packed-fp32-ops' is not a recognized feature"
     err = '\n'.join(l for l in proc.stderr.splitlines() if noise not in l)

@@ -7,7 +7,7 @@
 #include <stdint.h>
 #include <string>
 
-#include "../../include/localmoe35ba3b.h"
+#include "localmoe35ba3b.h"
 
 namespace lm {
 

@@ -38,7 +38,26 @@ struct GemmArgs {
   int N;
   int K;
   int tile_rows;  // rows covered by one table tile (<= BM)
+  int nt_count;   // column tiles
+  int mt_count;   // row tiles (table rows, or dense M tiles)
 };
+
+// Workgroups are dealt to the 8 XCDs round-robin by linear id.  Map linear
+// id b -> (row tile, column tile) so that all column tiles of one row tile
+// run on the same XCD back to back: the gathered activation rows of a tile
+// are then read from HBM/MALL once and served from that XCD's L2 for the
+// other column tiles.  Returns false for padding workgroups.
+__device__ __forceinline__ bool xcd_tile(const GemmArgs &a, int &mt, int &nt) {
+  const int b = blockIdx.x;
+  const int j = b >> 3;
+  mt = (j / a.nt_count) * 8 + (b & 7);
+  nt = j % a.nt_count;
+  return mt < a.mt_count;
+}
+
+static unsigned xcd_grid(int mtiles, int ntiles) {
+  return (unsigned)(8 * ntiles * ((mtiles + 7) / 8));
+}
 
 template <typename T, int BM, int WM, bool SWIGLU, bool GATHER, bool DENSE>
 __global__ __launch_bounds__(256) void w8a16_mfma_kernel(GemmArgs a) {
@@ -56,8 +75,8 @@ __global__ __launch_bounds__(256) void w8a16_mfma_kernel(GemmArgs a) {
   const int wave = tid >> 6;
   const int wm = wave / WN;
   const int wn = wave % WN;
-  const int nt = blockIdx.x;
-  const int mt = blockIdx.y;
+  int mt, nt;
+  if (!xcd_tile(a, mt, nt)) return;
 
   int64_t e = 0, start, stop;
   if constexpr (DENSE) {
@@ -207,11 +226,442 @@ __global__ __launch_bounds__(256) void w8a16_mfma_kernel(GemmArgs a) {
   }
 }
 
-template <typename T, int BM, int WM, bool SWIGLU, bool GATHER, bool DENSE>
-static int launch_gemm(const GemmArgs &a, unsigned mtiles, hipStream_t st) {
-  const int nt = SWIGLU ? (int)cdiv(a.N / 2, kBN / 2) : (int)cdiv(a.N, kBN);
+// Routed grouped GEMM (prefill MoE shape: ~64 routes per expert, up to 128
+// rows per tile so one tile covers a whole expert and its weights are read
+// and dequantized once).  Row sub-tiles of 16 beyond the tile's routes are
+// skipped entirely (no loads, no MFMA), so an expert with 70 routes costs
+// 80 rows of MFMA work.  The four waves split the BN columns; each wave keeps
+// its own int8 B fragments in LDS and dequantizes them exactly (T(q * s)) right
+// before the MFMA, once per workgroup per weight.  A and B of the next stage
+// are prefetched into registers while the current stage computes.
+constexpr int kGBM = 128;
+constexpr int kLDB = kBK + 8;  // int8 bytes per LDS row of the weight tile
+
+__device__ __forceinline__ u32x4 dequant8_bf16(uint2 w, float s) {
+  const float n = -128.0f * s;
+  float f[8];
+  dequant4(w.x, s, n, f);
+  dequant4(w.y, s, n, f + 4);
+  return u32x4{BF16::pack2(f[0], f[1]), BF16::pack2(f[2], f[3]), BF16::pack2(f[4], f[5]),
+               BF16::pack2(f[6], f[7])};
+}
+
+template <bool SWIGLU, bool GATHER, int BN>
+__global__ __launch_bounds__(256) void grouped_mfma_kernel(GemmArgs a) {
+  constexpr int TN = BN / 4;       // columns per wave
+  constexpr int MI = kGBM / 16;    // row sub-tiles
+  constexpr int NI = TN / 16;      // column sub-tiles per wave
+  constexpr int ACH = kGBM * 8 / 256;  // 16-byte A chunks per thread per stage
+  constexpr int BCH = BN * 4 / 256;    // 16-byte B chunks per thread per stage
+  __shared__ __align__(16) uint16_t As[kGBM * kLDA];
+  __shared__ __align__(16) int8_t Bs[BN * kLDB];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wn = tid >> 6;
+  int mt, nt;
+  if (!xcd_tile(a, mt, nt)) return;
+  const int64_t e = a.table[mt * 3];
+  const int64_t start = a.table[mt * 3 + 1];
+  const int64_t stop = a.table[mt * 3 + 2];
+  if (start >= stop) return;
+  const int rows = (int)min((int64_t)a.tile_rows, stop - start);
+  const int msub = (rows + 15) >> 4;  // live row sub-tiles
+  const int8_t *wq = a.q + e * a.q_es;
+  const float *wsc = a.s + e * a.s_es;
+  const int K = a.K;
+  const int G = K >> 7;
+  const int half = a.N >> 1;
+  const int n0 = SWIGLU ? nt * (BN / 2) : nt * BN;
+
+  auto wrow = [&](int c) -> int {
+    if constexpr (SWIGLU) {
+      const int j = n0 + (c & (BN / 2 - 1));
+      if (j >= half) return -1;
+      return c < BN / 2 ? j : half + j;
+    } else {
+      const int j = n0 + c;
+      return j < a.N ? j : -1;
+    }
+  };
+  auto col_base = [&](int ni) -> int {
+    if constexpr (SWIGLU) {
+      return ni < NI / 2 ? wn * (TN / 2) + ni * 16 : BN / 2 + wn * (TN / 2) + (ni - NI / 2) * 16;
+    } else {
+      return wn * TN + ni * 16;
+    }
+  };
+
+  const uint16_t *asrc[ACH];
+  bool aok[ACH];
+#pragma unroll
+  for (int i = 0; i < ACH; ++i) {
+    const int c = tid + 256 * i;
+    const int r = c >> 3;
+    aok[i] = r < rows;
+    const int64_t xr = aok[i] ? (GATHER ? a.pos[start + r] : start + r) : 0;
+    asrc[i] = a.x + xr * a.ldx + (c & 7) * 8;
+  }
+  const int8_t *bsrc[BCH];
+  bool bok[BCH];
+#pragma unroll
+  for (int i = 0; i < BCH; ++i) {
+    const int c = tid + 256 * i;
+    const int wr = wrow(c >> 2);
+    bok[i] = wr >= 0;
+    bsrc[i] = wq + (int64_t)(bok[i] ? wr : 0) * K + (c & 3) * 16;
+  }
+  const float *ssrc[NI];
+  bool sok[NI];
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni) {
+    const int wr = wrow(col_base(ni) + (lane & 15));
+    sok[ni] = wr >= 0;
+    ssrc[ni] = wsc + (int64_t)(sok[ni] ? wr : 0) * G;
+  }
+
+  u32x4 ra[ACH], rb[BCH];
+  float rs[NI];
+  auto prefetch = [&](int kt) {
+    const int k0 = kt * kBK;
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) ra[i] = aok[i] ? ldg16(asrc[i] + k0) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) rb[i] = bok[i] ? ldg16(bsrc[i] + k0) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) rs[ni] = sok[ni] ? ssrc[ni][k0 >> 7] : 0.0f;
+  };
+
+  f32x4 acc[MI][NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = K / kBK;
+  prefetch(0);
+  for (int kt = 0; kt < KT; ++kt) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i;
+      if (aok[i]) *reinterpret_cast<u32x4 *>(&As[(c >> 3) * kLDA + (c & 7) * 8]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i;
+      int8_t *bd = &Bs[(c >> 2) * kLDB + (c & 3) * 16];
+      *reinterpret_cast<uint2 *>(bd) = uint2{rb[i][0], rb[i][1]};
+      *reinterpret_cast<uint2 *>(bd + 8) = uint2{rb[i][2], rb[i][3]};
+    }
+    float sc[NI];
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) sc[ni] = rs[ni];
+    __syncthreads();
+    if (kt + 1 < KT) prefetch(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < kBK / 32; ++ks) {
+      const int kk = ks * 32 + (lane >> 4) * 8;
+      u32x4 bfr[NI];
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        bfr[ni] = dequant8_bf16(
+            *reinterpret_cast<const uint2 *>(&Bs[(col_base(ni) + (lane & 15)) * kLDB + kk]),
+            sc[ni]);
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
+        if (mi < msub) {
+          const u32x4 af =
+              *reinterpret_cast<const u32x4 *>(&As[(mi * 16 + (lane & 15)) * kLDA + kk]);
+#pragma unroll
+          for (int ni = 0; ni < NI; ++ni)
+            acc[mi][ni] = BF16::mfma16x16x32(af, bfr[ni], acc[mi][ni]);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+    if (mi >= msub) continue;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int rl = mi * 16 + (lane >> 4) * 4 + it;
+      if (rl >= rows) continue;
+      uint16_t *yrow = a.y + (start + rl) * a.ldy;
+      if constexpr (SWIGLU) {
+#pragma unroll
+        for (int ni = 0; ni < NI / 2; ++ni) {
+          const int col = n0 + wn * (TN / 2) + ni * 16 + (lane & 15);
+          if (col < half) {
+            const float gate = round_bf16(acc[mi][ni][it]);
+            const float up = round_bf16(acc[mi][ni + NI / 2][it]);
+            yrow[col] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+          const int col = n0 + col_base(ni) + (lane & 15);
+          if (col < a.N) yrow[col] = f32_to_bf16_bits(acc[mi][ni][it]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pipelined variant for the model's K (2048 gate_up, 512 down): a ring of
+// kRing LDS stages filled by direct global->LDS loads (global_load_lds_dwordx4,
+// 16 bytes per lane straight into LDS, no registers held), so each workgroup
+// keeps two stages (~48 KB) in flight while it computes the third.  Every wave
+// issues the same fixed number of loads per stage, which lets the
+// consumer wait with a constant s_waitcnt vmcnt.  LDS layout per stage:
+//   A  128 rows x 64 bf16 (128 B/row), 16-byte chunk p of row r holds the
+//      chunk p ^ (r & 7) of the source row
+//   B  128 cols x 64 int8 (64 B/col), chunk p of col c holds chunk
+//      p ^ ((c >> 1) & 3)
+// (the XOR swizzles spread the MFMA fragment reads over the LDS banks).  The
+// tile's scales [128 cols][K/128] are staged once, in the same load batch as
+// the first stages.  Rows of absent 8-row groups still load a valid row (the
+// tile's last) so the per-wave load count stays fixed; they are never read.
+#ifndef LM_PIPE_BM
+#define LM_PIPE_BM 96
+#endif
+#ifndef LM_PIPE_RING
+#define LM_PIPE_RING 2
+#endif
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+typedef const __attribute__((address_space(1))) void *gbl_ptr_t;
+
+// One 16-byte-per-lane global->LDS load: lane i writes LDS bytes
+// [base + 16 i, base + 16 i + 16).  Issued through inline asm so the
+// compiler's wait-count insertion does not treat every later LDS read as
+// depending on it (it cannot tell ring slots apart and would wait for all
+// loads in flight); the kernel waits for its loads explicitly (wait_vmcnt).
+__device__ __forceinline__ void load_lds16(const void *g, void *lds_wave_base) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(lds_ptr_t)lds_wave_base);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(base), "v"(g)
+               : "memory", "m0");
+}
+
+// Workgroup barrier without the release/acquire fences of __syncthreads():
+// those would make every wave wait for all of its outstanding global->LDS
+// loads.  Callers wait for exactly the loads they need (wait_vmcnt) first;
+// the memory clobber keeps the compiler from moving LDS accesses across.
+__device__ __forceinline__ void barrier_raw() { asm volatile("s_barrier" ::: "memory"); }
+
+// s_waitcnt with only the vector-memory counter constrained.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <bool SWIGLU, bool GATHER, int K, int BM, int kRing, int kBN>
+__global__ __launch_bounds__(256, 2) void grouped_lds_kernel(GemmArgs a) {
+  constexpr int kStageB = kBN * kBK;  // int8 weights per stage
+  constexpr int G = K / 128;
+  constexpr int KT = K / kBK;
+  constexpr int TN = kBN / 4;
+  constexpr int MI = BM / 16;
+  constexpr int NI = TN / 16;
+  constexpr int kStageA = BM * kBK * 2;
+  constexpr int kStage = kStageA + kStageB;
+  constexpr int A_INS = kStageA / 1024 / 4;  // A load instructions per wave per stage
+  constexpr int B_INS = kStageB / 1024 / 4;  // (2)
+  constexpr int PER_STAGE = A_INS + B_INS;
+  constexpr int SC_BYTES = kBN * G * 4;
+  constexpr int SC_INS = SC_BYTES >= 4096 ? SC_BYTES / 4096 : 1;  // per wave
+  __shared__ __align__(1024) unsigned char smem[kRing * kStage + SC_BYTES];
+  float *scl = reinterpret_cast<float *>(smem + kRing * kStage);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
+  int mt, nt;
+  if (!xcd_tile(a, mt, nt)) return;
+  const int64_t e = a.table[mt * 3];
+  const int64_t start = a.table[mt * 3 + 1];
+  const int64_t stop = a.table[mt * 3 + 2];
+  if (start >= stop) return;
+  const int rows = (int)min((int64_t)a.tile_rows, stop - start);
+  const int8_t *wq = a.q + e * a.q_es;
+  const float *wsc = a.s + e * a.s_es;
+  const int half = a.N >> 1;
+  const int n0 = SWIGLU ? nt * (kBN / 2) : nt * kBN;
+
+  auto wrow = [&](int c) -> int {
+    if constexpr (SWIGLU) {
+      const int j = n0 + (c & (kBN / 2 - 1));
+      if (j >= half) return -1;
+      return c < kBN / 2 ? j : half + j;
+    } else {
+      const int j = n0 + c;
+      return j < a.N ? j : -1;
+    }
+  };
+  auto col_base = [&](int ni) -> int {
+    if constexpr (SWIGLU) {
+      return ni < NI / 2 ? wave * (TN / 2) + ni * 16
+                         : kBN / 2 + wave * (TN / 2) + (ni - NI / 2) * 16;
+    } else {
+      return wave * TN + ni * 16;
+    }
+  };
+
+  // Per-lane sources of this wave's load instructions (stage offset k0 added later).
+  const uint16_t *asrc[A_INS];
+#pragma unroll
+  for (int j = 0; j < A_INS; ++j) {
+    const int ins = wave * A_INS + j;
+    const int r = ins * 8 + (lane >> 3);
+    const int rr = min(r, rows - 1);
+    const int64_t xr = GATHER ? a.pos[start + rr] : start + rr;
+    const int chunk = (lane & 7) ^ (r & 7);
+    asrc[j] = a.x + xr * a.ldx + chunk * 8;
+  }
+  const int8_t *bsrc[B_INS];
+#pragma unroll
+  for (int j = 0; j < B_INS; ++j) {
+    const int ins = wave * B_INS + j;
+    const int c = ins * 16 + (lane >> 2);
+    const int wr = wrow(c);
+    const int chunk = (lane & 3) ^ ((c >> 1) & 3);
+    bsrc[j] = wq + (int64_t)(wr >= 0 ? wr : 0) * K + chunk * 16;
+  }
+
+  auto issue_stage = [&](int kt) {
+    unsigned char *base = smem + (kt % kRing) * kStage;
+    const int k0 = kt * kBK;
+#pragma unroll
+    for (int j = 0; j < A_INS; ++j) load_lds16(asrc[j] + k0, base + (wave * A_INS + j) * 1024);
+#pragma unroll
+    for (int j = 0; j < B_INS; ++j)
+      load_lds16(bsrc[j] + k0, base + kStageA + (wave * B_INS + j) * 1024);
+  };
+
+  // Scales of the tile: [128 cols][G] floats.
+#pragma unroll
+  for (int j = 0; j < SC_INS; ++j) {
+    const int ins = (G * 16 >= 256) ? wave * SC_INS + j : (wave % (SC_BYTES / 1024));
+    const int lanes_per_col = G / 4;  // 16-byte pieces per column
+    const int c = (ins * 64 + lane) / lanes_per_col;
+    const int piece = (ins * 64 + lane) % lanes_per_col;
+    const int wr = wrow(c);
+    load_lds16(wsc + (int64_t)(wr >= 0 ? wr : 0) * G + piece * 4,
+               reinterpret_cast<unsigned char *>(scl) + ins * 1024);
+  }
+#pragma unroll
+  for (int s = 0; s < kRing - 1; ++s) issue_stage(s);
+
+  f32x4 acc[MI][NI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kt = 0; kt < KT; ++kt) {
+    if (kt + 1 < KT) wait_vmcnt<PER_STAGE * (kRing - 2)>();
+    else wait_vmcnt<0>();
+    barrier_raw();
+    if (kt + kRing - 1 < KT) issue_stage(kt + kRing - 1);
+    const unsigned char *sa = smem + (kt % kRing) * kStage;
+    const int8_t *sb = reinterpret_cast<const int8_t *>(sa + kStageA);
+    const int g = (kt * kBK) >> 7;
+    float sc[NI];
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) sc[ni] = scl[(col_base(ni) + (lane & 15)) * G + g];
+#pragma unroll
+    for (int ks = 0; ks < kBK / 32; ++ks) {
+      const int q = lane >> 4;
+      u32x4 bfr[NI];
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) {
+        const int c = col_base(ni) + (lane & 15);
+        const int pos = (ks * 2 + (q >> 1)) ^ ((c >> 1) & 3);
+        bfr[ni] = dequant8_bf16(*reinterpret_cast<const uint2 *>(sb + c * kBK + pos * 16 + (q & 1) * 8),
+                                sc[ni]);
+      }
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi) {
+        const int r = mi * 16 + (lane & 15);
+        const int pos = (ks * 4 + q) ^ (r & 7);
+        const u32x4 af = *reinterpret_cast<const u32x4 *>(sa + r * 128 + pos * 16);
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = BF16::mfma16x16x32(af, bfr[ni], acc[mi][ni]);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int rl = mi * 16 + (lane >> 4) * 4 + it;
+      if (rl >= rows) continue;
+      uint16_t *yrow = a.y + (start + rl) * a.ldy;
+      if constexpr (SWIGLU) {
+#pragma unroll
+        for (int ni = 0; ni < NI / 2; ++ni) {
+          const int col = n0 + wave * (TN / 2) + ni * 16 + (lane & 15);
+          if (col < half) {
+            const float gate = round_bf16(acc[mi][ni][it]);
+            const float up = round_bf16(acc[mi][ni + NI / 2][it]);
+            yrow[col] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+          const int col = n0 + col_base(ni) + (lane & 15);
+          if (col < a.N) yrow[col] = f32_to_bf16_bits(acc[mi][ni][it]);
+        }
+      }
+    }
+  }
+}
+
+#ifndef LM_GROUPED_BN
+#define LM_GROUPED_BN 128
+#endif
+#ifndef LM_PIPELINED
+#define LM_PIPELINED 1
+#endif
+
+template <bool SWIGLU, bool GATHER>
+static int launch_grouped(GemmArgs a, unsigned mtiles, hipStream_t st) {
+  constexpr int BN = LM_GROUPED_BN;
+  a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, BN / 2) : (int)cdiv(a.N, BN);
+  a.mt_count = (int)mtiles;
   if (mtiles == 0) return LM_OK;
-  w8a16_mfma_kernel<T, BM, WM, SWIGLU, GATHER, DENSE><<<dim3(nt, mtiles), 256, 0, st>>>(a);
+  const unsigned grid = xcd_grid(a.mt_count, a.nt_count);
+#if LM_PIPELINED
+  if (a.tile_rows <= LM_PIPE_BM && a.K == 2048) {
+    grouped_lds_kernel<SWIGLU, GATHER, 2048, LM_PIPE_BM, LM_PIPE_RING, BN><<<grid, 256, 0, st>>>(a);
+    return check_launch("grouped_lds_kernel");
+  }
+  if (a.tile_rows <= LM_PIPE_BM && a.K == 512) {
+    grouped_lds_kernel<SWIGLU, GATHER, 512, LM_PIPE_BM, LM_PIPE_RING, BN><<<grid, 256, 0, st>>>(a);
+    return check_launch("grouped_lds_kernel");
+  }
+#endif
+  grouped_mfma_kernel<SWIGLU, GATHER, BN><<<grid, 256, 0, st>>>(a);
+  return check_launch("grouped_mfma_kernel");
+}
+
+
+template <typename T, int BM, int WM, bool SWIGLU, bool GATHER, bool DENSE>
+static int launch_gemm(GemmArgs a, unsigned mtiles, hipStream_t st) {
+  a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, kBN / 2) : (int)cdiv(a.N, kBN);
+  a.mt_count = (int)mtiles;
+  if (mtiles == 0) return LM_OK;
+  w8a16_mfma_kernel<T, BM, WM, SWIGLU, GATHER, DENSE>
+      <<<xcd_grid(a.mt_count, a.nt_count), 256, 0, st>>>(a);
   return check_launch("w8a16_mfma_kernel");
 }
 
@@ -253,18 +703,9 @@ int routed_gemm(const void *x, const int8_t *q, const float *s, const int64_t *p
   a.K = (int)k;
   a.tile_rows = (int)bm;
   const unsigned mt = (unsigned)n_tiles;
-  if (bm <= 64) {
-    if (swiglu)
-      return gather ? launch_gemm<BF16, 64, 1, true, true, false>(a, mt, st)
-                    : launch_gemm<BF16, 64, 1, true, false, false>(a, mt, st);
-    return gather ? launch_gemm<BF16, 64, 1, false, true, false>(a, mt, st)
-                  : launch_gemm<BF16, 64, 1, false, false, false>(a, mt, st);
-  }
   if (swiglu)
-    return gather ? launch_gemm<BF16, 128, 2, true, true, false>(a, mt, st)
-                  : launch_gemm<BF16, 128, 2, true, false, false>(a, mt, st);
-  return gather ? launch_gemm<BF16, 128, 2, false, true, false>(a, mt, st)
-                : launch_gemm<BF16, 128, 2, false, false, false>(a, mt, st);
+    return gather ? launch_grouped<true, true>(a, mt, st) : launch_grouped<true, false>(a, mt, st);
+  return gather ? launch_grouped<false, true>(a, mt, st) : launch_grouped<false, false>(a, mt, st);
 }
 
 int w8a16_gemv_dense(const void *x, const int8_t *q, const float *s, void *y, int64_t m,

@@ -79,11 +79,19 @@ __device__ __forceinline__ void stream_rows(int R, int G, RowPtr row_ptr, Body b
 template <int LOADS>
 struct RowLoads {
   u32x4 w[LOADS];
+  float s[LOADS];  // per-load group scale (issue_scaled only)
   int r[LOADS], g[LOADS], f[LOADS];
   bool ok[LOADS];
 
   template <typename RowPtr>
   __device__ __forceinline__ void issue(int R, int G, RowPtr row_ptr) {
+    issue_scaled(R, G, row_ptr, [](int) -> const float * { return nullptr; });
+  }
+
+  // Also loads the fp32 scale of each (row, group) next to its weights, so
+  // no second round trip is needed for the scales.
+  template <typename RowPtr, typename ScalePtr>
+  __device__ __forceinline__ void issue_scaled(int R, int G, RowPtr row_ptr, ScalePtr scale_ptr) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nwaves = blockDim.x >> 6;
@@ -103,6 +111,8 @@ struct RowLoads {
       g[u] = gg;
       f[u] = ff;
       w[u] = ok[u] ? ldg16(row_ptr(rr) + gg * 128 + sub * 16) : u32x4{0u, 0u, 0u, 0u};
+      const float *sp = scale_ptr(rr);
+      s[u] = (ok[u] && sp) ? sp[gg] : 0.0f;
       ff += 8;
       gg += 8;
       while (gg >= G) {
@@ -116,6 +126,13 @@ struct RowLoads {
   __device__ __forceinline__ void consume(Body body) {
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) body(w[u], r[u], g[u], f[u], ok[u]);
+  }
+
+  // body(w, scale, r, g, f, ok)
+  template <typename Body>
+  __device__ __forceinline__ void consume_scaled(Body body) {
+#pragma unroll
+    for (int u = 0; u < LOADS; ++u) body(w[u], s[u], r[u], g[u], f[u], ok[u]);
   }
 };
 

@@ -25,7 +25,7 @@ constexpr int kH = 2048;
 constexpr int kI = 512;
 constexpr int kE = 256;
 constexpr int kTopK = 8;
-constexpr int kBM = 64;  // prefill MFMA tile height
+constexpr int kBM = 96;  // prefill MFMA tile height (one tile covers a typical expert)
 
 struct WsLayout {
   int64_t ctr, xn, gl, logits, ids, wts, sel, selw, xq, xs, pos, table, ordered, slots, hbuf,
@@ -138,28 +138,49 @@ __device__ __forceinline__ double dot_lds_f64(const float *xf, const uint16_t *w
   return wave_sum_f64(acc);
 }
 
+// Router logits of the decode token: blocks 0..E/4-1 take one expert per
+// wave (the router row is loaded before the RMSNorm so its HBM latency
+// overlaps the norm); block E/4 writes the normalized row, its W8A8
+// quantization and the shared-expert gate logit.  No inter-block sync.
 __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
   __shared__ float xf[kH];
   __shared__ float red[4];
-  __shared__ float lgs[kE];
-  __shared__ int64_t sid[kTopK];
-  __shared__ uint16_t swt[kTopK];
-  __shared__ int is_last;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
+  const bool routed = blockIdx.x < kE / 4;
+  const int e = blockIdx.x * 4 + wave;
+  const uint16_t *wrow = routed ? a.router_w + (int64_t)e * kH : a.gate_w;
+  u32x4 wv[kH / 512];
+#pragma unroll
+  for (int j = 0; j < kH / 512; ++j) wv[j] = ldg16(wrow + lane * 8 + j * 512);
   norm_row_to_lds(a.h, a.norm_w, a.eps, xf, red);
 
-  if (blockIdx.x < kE / 4) {
-    const int e = blockIdx.x * 4 + wave;
-    const double s = dot_lds_f64(xf, a.router_w + (int64_t)e * kH, lane);
-    if (lane == 0) {
-      float l = round_bf16((float)s);
-      if (a.router_bias) l = l + a.router_bias[e];
-      a.logits[e] = l;
+  if (routed || wave == 0) {
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 0; j < kH / 512; ++j) {
+      const int k0 = lane * 8 + j * 512;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc = __builtin_fma((double)xf[k0 + 2 * i], (double)bf16_bits_to_f32(wv[j][i] & 0xFFFFu),
+                            acc);
+        acc = __builtin_fma((double)xf[k0 + 2 * i + 1], (double)bf16_bits_to_f32(wv[j][i] >> 16),
+                            acc);
+      }
     }
-  } else {
-    // normalized row, its W8A8 quantization, and the shared-expert gate logit
+    acc = wave_sum_f64(acc);
+    if (lane == 0) {
+      float l = round_bf16((float)acc);
+      if (routed) {
+        if (a.router_bias) l = l + a.router_bias[e];
+        a.logits[e] = l;
+      } else {
+        a.gl[0] = l;
+      }
+    }
+  }
+  if (!routed) {
     for (int i = t; i < kH; i += 256) a.xn[i] = f32_to_bf16_bits(xf[i]);
     const int half = t >> 5, l = t & 31;
     const float inv127 = (float)(1.0 / 127.0);
@@ -178,35 +199,37 @@ __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
       *reinterpret_cast<uint32_t *>(a.xq + g * 128 + l * 4) = packed;
       if (l == 0) a.xs[g] = sc;
     }
-    if (wave == 0) {
-      const double s = dot_lds_f64(xf, a.gate_w, lane);
-      if (lane == 0) a.gl[0] = round_bf16((float)s);
-    }
   }
+}
 
-  // Last workgroup to finish: top-k over all logits.
-  __threadfence();
+// Top-8 of the decode token from the router logits (one wave), ascending
+// expert order for the combine.  Every decode gate_up workgroup runs it on
+// the same inputs, so all of them agree bit for bit; workgroup (0, 0)
+// publishes the result for the down kernel and the caller.
+__device__ __forceinline__ void decode_topk(const LayerArgs &a, float *lgs, int *sel, float *selw) {
+  __shared__ int64_t sid[kTopK];
+  __shared__ uint16_t swt[kTopK];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  lgs[t] = a.logits[t];
   __syncthreads();
-  if (t == 0) is_last = atomicAdd(a.ctr, 1) == (int)gridDim.x - 1;
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  for (int e = t; e < kE; e += 256) lgs[e] = ld_coherent(a.logits + e);
-  __syncthreads();
-  if (wave == 0) {
+  if (t < 64) {
     topk_wave(lgs, kE, kTopK, lane, sid, swt);
     if (lane == 0) {
       int ids[kTopK];
       float w[kTopK];
+      const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
       for (int i = 0; i < kTopK; ++i) {
         ids[i] = (int)sid[i];
         w[i] = bf16_bits_to_f32(swt[i]);
-        a.ids[i] = sid[i];
-        a.wts[i] = swt[i];
-        if (a.ids_out) a.ids_out[i] = ids[i];
-        if (a.wts_out) a.wts_out[i] = swt[i];
+        if (pub) {
+          a.ids[i] = sid[i];
+          a.wts[i] = swt[i];
+          if (a.ids_out) a.ids_out[i] = ids[i];
+          if (a.wts_out) a.wts_out[i] = swt[i];
+        }
       }
-      for (int i = 1; i < kTopK; ++i) {  // ascending expert id (combine order)
+      for (int i = 1; i < kTopK; ++i) {
         const int ki = ids[i];
         const float wi = w[i];
         int m = i - 1;
@@ -219,87 +242,90 @@ __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
         w[m + 1] = wi;
       }
       for (int i = 0; i < kTopK; ++i) {
-        a.sel[i] = ids[i];
-        a.selw[i] = w[i];
+        sel[i] = ids[i];
+        selw[i] = w[i];
+        if (pub) {
+          a.sel[i] = ids[i];
+          a.selw[i] = w[i];
+        }
       }
-      __hip_atomic_store(a.ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  __syncthreads();
 }
 
 // gate_up of slot blockIdx.y (0..7 routed W8A8, 8 = shared W8A16), 8 output
-// columns per block: rows n0..n0+7 (gate) and kI+n0.. (up), K = kH.
+// columns per block: rows n0..n0+7 (gate) and kI+n0.. (up), K = kH.  The W8A8
+// per-group terms (f32(p) * xs_g) * ws_g are formed by the lane that owns the
+// partial and summed in ascending group order by the epilogue (w8a8.py:40).
 constexpr int kGuPairs = 8;
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
   constexpr int G = kH / 128;
   constexpr int R = 2 * kGuPairs;
   __shared__ __align__(16) unsigned char xbuf[kH * 2];
   __shared__ float xs[G];
-  __shared__ float ws[R * G];
-  __shared__ float partf[R * G];
-  __shared__ int parti[R * G];
+  __shared__ float term[R * G];
+  __shared__ float lgs[kE];
+  __shared__ int sel[kTopK];
+  __shared__ float selw[kTopK];
+  const int t = threadIdx.x;
   const int slot = blockIdx.y;
   const bool shared = slot == kTopK;
   const int n0 = blockIdx.x * kGuPairs;
-  const int e = shared ? kE : a.sel[slot];
-  const int8_t *wq = a.gu_q + (int64_t)e * a.gu_qes;
-  const float *wsrc = a.gu_s + (int64_t)e * a.gu_ses;
   const RowMap map{n0, kI + n0, kGuPairs};
   RowLoads<8> L;
-  L.issue(R, G, [&](int r) { return wq + (int64_t)map(r) * kH; });
-
-  const int t = threadIdx.x;
+  auto issue = [&](int e) {
+    const int8_t *wq = a.gu_q + (int64_t)e * a.gu_qes;
+    const float *ws = a.gu_s + (int64_t)e * a.gu_ses;
+    L.issue_scaled(
+        R, G, [&](int r) { return wq + (int64_t)map(r) * kH; },
+        [&](int r) { return ws + (int64_t)map(r) * G; });
+  };
+  if (shared) issue(kE);  // independent of the routing: start at once
+  decode_topk(a, lgs, sel, selw);
+  if (!shared) issue(sel[slot]);
   if (shared) {
-    for (int i = t; i < kH / 8; i += 256)
-      reinterpret_cast<u32x4 *>(xbuf)[i] = ldg16(a.xn + i * 8);
+    reinterpret_cast<u32x4 *>(xbuf)[t] = ldg16(a.xn + t * 8);
   } else {
-    for (int i = t; i < kH / 16; i += 256)
-      reinterpret_cast<u32x4 *>(xbuf)[i] = ldg16(a.xq + i * 16);
+    if (t < kH / 16) reinterpret_cast<u32x4 *>(xbuf)[t] = ldg16(a.xq + t * 16);
     if (t < G) xs[t] = a.xs[t];
   }
-  for (int i = t; i < R * G; i += 256) ws[i] = wsrc[(int64_t)map(i / G) * G + (i % G)];
   __syncthreads();
 
   const int sub = t & 7;
   if (shared) {
     const uint16_t *x16 = reinterpret_cast<const uint16_t *>(xbuf);
-    L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
+    L.consume_scaled([&](u32x4 w, float sc, int r, int g, int f, bool ok) {
       uint32_t wd[8];
-      dequant16<BF16>(w, ok ? ws[f] : 0.0f, wd);
+      dequant16<BF16>(w, sc, wd);
       const uint16_t *xp = x16 + g * 128 + sub * 16;
       const float p = octet_sum_f32(dot16_w16<BF16>(wd, *reinterpret_cast<const u32x4 *>(xp),
                                                     *reinterpret_cast<const u32x4 *>(xp + 8)));
-      if (ok && sub == 0) partf[f] = p;
+      if (ok && sub == 0) term[f] = p;
     });
   } else {
     const int8_t *x8 = reinterpret_cast<const int8_t *>(xbuf);
-    L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
+    L.consume_scaled([&](u32x4 w, float sc, int r, int g, int f, bool ok) {
       const int p = octet_sum_i32(
           dot16_i8(w, *reinterpret_cast<const u32x4 *>(x8 + g * 128 + sub * 16)));
-      if (ok && sub == 0) parti[f] = p;
+      if (ok && sub == 0) term[f] = mul_rn(mul_rn((float)p, xs[g]), sc);
     });
   }
   __syncthreads();
   if (t < kGuPairs) {
-    float gate, up;
-    if (shared) {
-      float sg = 0.0f, su = 0.0f;
-      for (int g = 0; g < G; ++g) {
-        sg += partf[t * G + g];
-        su += partf[(kGuPairs + t) * G + g];
-      }
-      gate = round_bf16(sg);
-      up = round_bf16(su);
-    } else {
-      gate = round_bf16(w8a8_epilogue(parti + t * G, xs, ws + t * G, G));
-      up = round_bf16(w8a8_epilogue(parti + (kGuPairs + t) * G, xs, ws + (kGuPairs + t) * G, G));
+    float sg = 0.0f, su = 0.0f;
+    for (int g = 0; g < G; ++g) {
+      sg = add_rn(sg, term[t * G + g]);
+      su = add_rn(su, term[(kGuPairs + t) * G + g]);
     }
+    const float gate = round_bf16(sg), up = round_bf16(su);
     a.hbuf[slot * kI + n0 + t] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
   }
 }
 
 // down rows of all 9 slots for 8 output columns, combine, gated shared add,
-// residual add.
+// residual add.  The 8 routed SwiGLU rows are quantized per row (w8a8.quantize
+// on [8, kI]) in one parallel pass: thread t owns 16 values of row t / 32.
 constexpr int kDnCols = 8;
 __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   constexpr int G = kI / 128;
@@ -307,52 +333,81 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   __shared__ __align__(16) int8_t xq[kTopK * kI];
   __shared__ float xs[kTopK * G];
   __shared__ __align__(16) uint16_t xsh[kI];
-  __shared__ float ws[R * G];
-  __shared__ int parti[kTopK * kDnCols * G];
-  __shared__ float partf[kDnCols * G];
+  __shared__ float term[R * G];
+  __shared__ float selw[kTopK];
   const int t = threadIdx.x;
   const int c0 = blockIdx.x * kDnCols;
   int ex[kTopK + 1];
 #pragma unroll
   for (int s = 0; s < kTopK; ++s) ex[s] = a.sel[s];
   ex[kTopK] = kE;
-  auto rowp = [&](int r) {
+  auto expert_of = [&](int r) {
     const int s = r / kDnCols;
     int e = kE;
 #pragma unroll
     for (int j = 0; j < kTopK; ++j)
       if (s == j) e = ex[j];
-    return a.dn_q + (int64_t)e * a.dn_qes + (int64_t)(c0 + r % kDnCols) * kI;
+    return e;
   };
   RowLoads<12> L;
-  L.issue(R, G, rowp);
+  L.issue_scaled(
+      R, G,
+      [&](int r) {
+        return a.dn_q + (int64_t)expert_of(r) * a.dn_qes + (int64_t)(c0 + r % kDnCols) * kI;
+      },
+      [&](int r) {
+        return a.dn_s + (int64_t)expert_of(r) * a.dn_ses + (int64_t)(c0 + r % kDnCols) * G;
+      });
 
-  // Row-quantize the 8 routed SwiGLU outputs (w8a8.quantize on [8, kI]).
-  quantize_rows_to_lds<BF16>(a.hbuf, kI, kTopK, kI, xq, xs);
-  for (int i = t; i < kI / 8; i += 256)
-    reinterpret_cast<u32x4 *>(xsh)[i] = ldg16(a.hbuf + kTopK * kI + i * 8);
-  for (int i = t; i < R * G; i += 256) {
-    const int r = i / G, g = i % G;
-    const int s = r / kDnCols;
-    const int e = s < kTopK ? a.sel[s] : kE;
-    ws[i] = a.dn_s[(int64_t)e * a.dn_ses + (int64_t)(c0 + r % kDnCols) * G + g];
+  // Row quantization of hbuf[0..7]: 16 values per thread, a 128-group is
+  // spread over 8 consecutive lanes.
+  const int row = t >> 5, col = (t & 31) * 16;
+  const u32x4 h0 = ldg16(a.hbuf + row * kI + col);
+  const u32x4 h1 = ldg16(a.hbuf + row * kI + col + 8);
+  if (t < kI / 8) reinterpret_cast<u32x4 *>(xsh)[t] = ldg16(a.hbuf + kTopK * kI + t * 8);
+  if (t < kTopK) selw[t] = a.selw[t];
+  float v[16];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = bf16_bits_to_f32(h0[j] & 0xFFFFu);
+    v[2 * j + 1] = bf16_bits_to_f32(h0[j] >> 16);
+    v[8 + 2 * j] = bf16_bits_to_f32(h1[j] & 0xFFFFu);
+    v[8 + 2 * j + 1] = bf16_bits_to_f32(h1[j] >> 16);
   }
+  float am = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) am = fmaxf(am, fabsf(v[j]));
+  am = fmaxf(am, __shfl_xor(am, 1, 64));
+  am = fmaxf(am, __shfl_xor(am, 2, 64));
+  am = fmaxf(am, __shfl_xor(am, 4, 64));
+  const float sc = fmaxf(am, 1e-10f) * (float)(1.0 / 127.0);
+  u32x4 packed;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t pk = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      pk |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[4 * j + i] / sc)) << (8 * i);
+    packed[j] = pk;
+  }
+  *reinterpret_cast<u32x4 *>(xq + row * kI + col) = packed;
+  if ((t & 7) == 0) xs[row * G + col / 128] = sc;
   __syncthreads();
 
   const int sub = t & 7;
-  L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
+  L.consume_scaled([&](u32x4 w, float scl, int r, int g, int f, bool ok) {
     const int s = r / kDnCols;  // uniform across the wave instruction
     if (s < kTopK) {
       const int p = octet_sum_i32(
           dot16_i8(w, *reinterpret_cast<const u32x4 *>(xq + s * kI + g * 128 + sub * 16)));
-      if (ok && sub == 0) parti[f] = p;
+      if (ok && sub == 0) term[f] = mul_rn(mul_rn((float)p, xs[s * G + g]), scl);
     } else {
       uint32_t wd[8];
-      dequant16<BF16>(w, ok ? ws[f] : 0.0f, wd);
+      dequant16<BF16>(w, scl, wd);
       const uint16_t *xp = xsh + g * 128 + sub * 16;
       const float p = octet_sum_f32(dot16_w16<BF16>(wd, *reinterpret_cast<const u32x4 *>(xp),
                                                     *reinterpret_cast<const u32x4 *>(xp + 8)));
-      if (ok && sub == 0) partf[f - kTopK * kDnCols * G] = p;
+      if (ok && sub == 0) term[f] = p;
     }
   });
   __syncthreads();
@@ -360,11 +415,12 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
     float acc = 0.0f;
     for (int s = 0; s < kTopK; ++s) {
       const int r = s * kDnCols + t;
-      const float v = round_bf16(w8a8_epilogue(parti + r * G, xs + s * G, ws + r * G, G));
-      acc = round_bf16(acc + round_bf16(v * a.selw[s]));
+      float v8 = 0.0f;
+      for (int g = 0; g < G; ++g) v8 = add_rn(v8, term[r * G + g]);
+      acc = round_bf16(acc + round_bf16(round_bf16(v8) * selw[s]));
     }
     float vs = 0.0f;
-    for (int g = 0; g < G; ++g) vs += partf[t * G + g];
+    for (int g = 0; g < G; ++g) vs += term[(kTopK * kDnCols + t) * G + g];
     const float vsh = round_bf16(vs);
     const float sig = round_bf16(sigmoid_f32(a.gl[0]));
     const float out = round_bf16(acc + round_bf16(sig * vsh));

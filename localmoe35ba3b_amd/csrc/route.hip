@@ -4,6 +4,8 @@
 //   device route plan: stable token sort / permute  (gpu_routes.py:17-63)
 //   ordered combines for decode and prefill         (int8.py:240-250, prefill.py:37-49)
 //   SwiGLU glue, RMSNorm                            (HF:715, HF:801-815)
+#include <type_traits>
+
 #include "internal.hpp"
 
 namespace lm {
@@ -158,8 +160,23 @@ int router_topk(const float *logits, int64_t T, int64_t E, int64_t K, int64_t *i
 }
 
 // ============================================================ route plan
-// Exclusive scan of v[0..255] held one per thread (256 threads); returns the
-// exclusive prefix and writes the total to *total.
+// Stable counting sort of the flat route ids by expert, one 1024-thread block.
+// Wave w owns a contiguous slice of the routes and walks it 64 at a time:
+// lanes holding the same expert id find each other with eight ballots over
+// the id bits, so a route's rank among equal ids inside the slice is the
+// wave's running count for that expert plus the equal ids in lower lanes.
+// A column scan over the 16 per-wave counts and a scan over experts turn
+// these slice ranks into positions of the stable order - three block
+// barriers in total.  ids are clamped into [0, E), so a malformed id can
+// never index out of bounds.
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanWaves = kPlanThreads / 64;
+// Routes per call whose ids and ranks are staged in LDS (ids as bytes,
+// ranks as 16-bit); larger calls keep the ranks in the `ordered` output.
+constexpr int kPlanLdsRoutes = 40960;
+
+// Exclusive scan of one value per thread over the first 256 threads of a
+// 1024-thread block (the others pass 0); returns the prefix, *total = sum.
 __device__ int block_scan_256(int v, int *scratch, int *total) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -169,94 +186,140 @@ __device__ int block_scan_256(int v, int *scratch, int *total) {
     const int u = __shfl_up(incl, o, 64);
     if (lane >= o) incl += u;
   }
-  if (lane == 63) scratch[wave] = incl;
+  if (lane == 63 && wave < 4) scratch[wave] = incl;
   __syncthreads();
   int base = 0;
-  for (int i = 0; i < wave; ++i) base += scratch[i];
+  for (int i = 0; i < wave && i < 4; ++i) base += scratch[i];
   const int all = scratch[0] + scratch[1] + scratch[2] + scratch[3];
   __syncthreads();
   *total = all;
   return base + incl - v;
 }
 
-constexpr int kPlanThreads = 256;
-constexpr int kPlanPerThread = 64;
-constexpr int kPlanChunk = kPlanThreads * kPlanPerThread;
+// Stable sort of up to N (id, slot, value) triples by id with an odd-even
+// transposition network (static register indices only).
+template <int N>
+__device__ __forceinline__ void sort_triples(int (&id)[N], int (&sl)[N], int (&v)[N]) {
+#pragma unroll
+  for (int pass = 0; pass < N; ++pass) {
+#pragma unroll
+    for (int i = pass & 1; i + 1 < N; i += 2) {
+      if (id[i] > id[i + 1]) {
+        const int a = id[i], b = sl[i], c = v[i];
+        id[i] = id[i + 1];
+        sl[i] = sl[i + 1];
+        v[i] = v[i + 1];
+        id[i + 1] = a;
+        sl[i + 1] = b;
+        v[i + 1] = c;
+      }
+    }
+  }
+}
 
-__global__ __launch_bounds__(256) void route_plan_kernel(const int64_t *__restrict__ ids, int T,
-                                                         int K, int E, int bm,
-                                                         int64_t *__restrict__ pos,
-                                                         int64_t *__restrict__ table,
-                                                         int max_tiles,
-                                                         int64_t *__restrict__ ordered,
-                                                         int64_t *__restrict__ slots,
-                                                         int shared_rows) {
-  __shared__ uint16_t cnt[kPlanThreads * 256];  // [thread][expert] counts, then prefixes
-  __shared__ int total[256], offs[257], carry[256], tends[256], scratch[4];
+template <bool LDS>
+__global__ __launch_bounds__(1024) void route_plan_kernel(const int64_t *__restrict__ ids, int T,
+                                                          int K, int E, int bm,
+                                                          int64_t *__restrict__ pos,
+                                                          int64_t *__restrict__ table,
+                                                          int max_tiles,
+                                                          int64_t *__restrict__ ordered,
+                                                          int64_t *__restrict__ slots,
+                                                          int shared_rows) {
+  __shared__ int offs[257], tends[256], scratch[4];
+  __shared__ int wcnt[kPlanWaves][256];
+  __shared__ uint8_t sid8[LDS ? kPlanLdsRoutes : 1];
+  __shared__ uint16_t srank[LDS ? kPlanLdsRoutes : 1];
   const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
   const int R = T * K;
-  auto eid = [&](int i) -> int {
-    int64_t e = ids[i];
-    return (int)(e < 0 ? 0 : (e >= E ? E - 1 : e));  // never index out of bounds
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  auto load_eid = [&](int i) -> int {
+    const int64_t e = ids[i];
+    return (int)(e < 0 ? 0 : (e >= E ? E - 1 : e));
   };
+  auto eid = [&](int i) -> int {
+    if constexpr (LDS) return sid8[i];
+    else return load_eid(i);
+  };
+  auto rank_get = [&](int r) -> int {
+    if constexpr (LDS) return srank[r];
+    else return (int)ordered[r];
+  };
+  auto rank_set = [&](int r, int v) {
+    if constexpr (LDS) srank[r] = (uint16_t)v;
+    else ordered[r] = v;
+  };
+  if constexpr (LDS) {
+#pragma unroll 8
+    for (int r = t; r < R; r += kPlanThreads) sid8[r] = (uint8_t)load_eid(r);
+  }
+  if (t < 256)
+    for (int w = 0; w < kPlanWaves; ++w) wcnt[w][t] = 0;
+  __syncthreads();
 
-  total[t] = 0;
-  carry[t] = 0;
+  // Pass 1: rank of every route among equal ids of its wave's slice.
+  const int slice = ((R + kPlanWaves - 1) / kPlanWaves + 63) & ~63;
+  const int lo = wave * slice, hi = min(lo + slice, R);
+  for (int base = lo; base < hi; base += 64) {
+    const int r = base + lane;
+    const bool valid = r < hi;
+    const int e = valid ? eid(r) : 0;
+    unsigned long long same = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const unsigned long long bit = __ballot(valid && ((e >> b) & 1));
+      same &= ((e >> b) & 1) ? bit : ~bit;
+    }
+    const int in_chunk = __popcll(same & lt);
+    const int before = valid ? wcnt[wave][e] : 0;
+    if (valid) rank_set(r, before + in_chunk);
+    if (valid && in_chunk == 0) wcnt[wave][e] = before + __popcll(same);
+  }
   __syncthreads();
-  for (int i = t; i < R; i += kPlanThreads) atomicAdd(&total[eid(i)], 1);
-  __syncthreads();
+  // Column scan: wcnt[w][e] becomes the count of e in slices before w.
+  int total_e = 0;
+  if (t < 256) {
+    for (int w = 0; w < kPlanWaves; ++w) {
+      const int c = wcnt[w][t];
+      wcnt[w][t] = total_e;
+      total_e += c;
+    }
+  }
   int all;
-  const int ex = block_scan_256(t < E ? total[t] : 0, scratch, &all);
-  offs[t] = ex;
+  const int ex = block_scan_256(t < E ? total_e : 0, scratch, &all);
+  if (t < 256) offs[t] = ex;
   if (t == 0) offs[256] = all;
   __syncthreads();
 
-  for (int base = 0; base < R; base += kPlanChunk) {
-    const int lo = base + t * kPlanPerThread;
-    const int hi = min(lo + kPlanPerThread, R);
-    uint16_t *mine = cnt + t * 256;
-    for (int e = 0; e < 256; e += 2) *reinterpret_cast<uint32_t *>(mine + e) = 0u;
-    for (int i = lo; i < hi; ++i) mine[eid(i)]++;
-    __syncthreads();
-    int run = 0;
-    if (t < E) {
-      for (int tt = 0; tt < kPlanThreads; ++tt) {
-        const int c = cnt[tt * 256 + t];
-        cnt[tt * 256 + t] = (uint16_t)run;
-        run += c;
-      }
-    }
-    __syncthreads();
-    for (int i = lo; i < hi; ++i) {
-      const int e = eid(i);
-      const int p = offs[e] + carry[e] + mine[e]++;
-      pos[p] = i / K;
-      ordered[i] = p;  // inverse permutation, consumed below
-    }
-    __syncthreads();
-    if (t < E) carry[t] += run;
-    __syncthreads();
+  // Pass 2: sorted position p of every route; pos[p] = its token.
+  for (int r = t; r < R; r += kPlanThreads) {
+    const int e = eid(r);
+    const int p = offs[e] + wcnt[r / slice][e] + rank_get(r);
+    pos[p] = r / K;
+    rank_set(r, p);
   }
 
   // Tile table (gpu_routes._table): tiles of bm rows, expert by expert.
   const int nt = t < E ? (offs[t + 1] - offs[t] + bm - 1) / bm : 0;
   int ntot;
   const int tex = block_scan_256(nt, scratch, &ntot);
-  tends[t] = tex + nt;
+  if (t < 256) tends[t] = tex + nt;
   __syncthreads();
   for (int i = t; i < max_tiles; i += kPlanThreads) {
     int64_t ex_ = 0, st_ = 0, sp_ = 0;
     if (i < ntot) {
-      int lo = 0, hi = E;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (tends[mid] <= i) lo = mid + 1;
-        else hi = mid;
+      int l = 0, h = E;
+      while (l < h) {
+        const int mid = (l + h) >> 1;
+        if (tends[mid] <= i) l = mid + 1;
+        else h = mid;
       }
-      const int prior = lo > 0 ? tends[lo - 1] : 0;
-      ex_ = lo;
-      st_ = offs[lo] + (int64_t)(i - prior) * bm;
-      sp_ = offs[lo + 1];
+      const int prior = l > 0 ? tends[l - 1] : 0;
+      ex_ = l;
+      st_ = offs[l] + (int64_t)(i - prior) * bm;
+      sp_ = offs[l + 1];
     }
     table[i * 3] = ex_;
     table[i * 3 + 1] = st_;
@@ -277,37 +340,42 @@ __global__ __launch_bounds__(256) void route_plan_kernel(const int64_t *__restri
   __syncthreads();
 
   // slots = argsort(ids, dim=1, stable); ordered[t, i] = inverse[t*K + slots[t, i]].
-  for (int tok = t; tok < T; tok += kPlanThreads) {
-    int sid[16], sl[16];
-    int64_t inv[16];
-    for (int j = 0; j < K; ++j) {
-      sid[j] = eid(tok * K + j);
-      sl[j] = j;
-      inv[j] = ordered[(int64_t)tok * K + j];
-    }
-    for (int j = 1; j < K; ++j) {  // stable insertion sort by id
-      const int ki = sid[j], si = sl[j];
-      int m = j - 1;
-      while (m >= 0 && sid[m] > ki) {
-        sid[m + 1] = sid[m];
-        sl[m + 1] = sl[m];
-        --m;
+  auto token_order = [&](auto n_tag) {
+    constexpr int N = decltype(n_tag)::value;
+    for (int tok = t; tok < T; tok += kPlanThreads) {
+      int id[N], sl[N], iv[N];
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        const bool in = j < K;
+        id[j] = in ? eid(tok * K + j) : 0x7FFFFFFF;
+        sl[j] = j;
+        iv[j] = in ? rank_get(tok * K + j) : 0;
       }
-      sid[m + 1] = ki;
-      sl[m + 1] = si;
+      sort_triples<N>(id, sl, iv);
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        if (j < K) {
+          slots[(int64_t)tok * K + j] = sl[j];
+          ordered[(int64_t)tok * K + j] = iv[j];
+        }
+      }
     }
-    for (int j = 0; j < K; ++j) {
-      slots[(int64_t)tok * K + j] = sl[j];
-      ordered[(int64_t)tok * K + j] = inv[sl[j]];
-    }
-  }
+  };
+  if (K <= 8) token_order(std::integral_constant<int, 8>{});
+  else token_order(std::integral_constant<int, 16>{});
 }
 
 int route_plan(const int64_t *ids, int64_t T, int64_t K, int64_t E, int64_t bm, int64_t *pos,
                int64_t *table, int64_t max_tiles, int64_t *ordered, int64_t *slots,
                int64_t shared_rows, hipStream_t st) {
-  route_plan_kernel<<<1, kPlanThreads, 0, st>>>(ids, (int)T, (int)K, (int)E, (int)bm, pos, table,
-                                                (int)max_tiles, ordered, slots, (int)shared_rows);
+  if (T * K <= kPlanLdsRoutes)
+    route_plan_kernel<true><<<1, kPlanThreads, 0, st>>>(ids, (int)T, (int)K, (int)E, (int)bm, pos,
+                                                        table, (int)max_tiles, ordered, slots,
+                                                        (int)shared_rows);
+  else
+    route_plan_kernel<false><<<1, kPlanThreads, 0, st>>>(ids, (int)T, (int)K, (int)E, (int)bm,
+                                                         pos, table, (int)max_tiles, ordered,
+                                                         slots, (int)shared_rows);
   return check_launch("route_plan_kernel");
 }
 

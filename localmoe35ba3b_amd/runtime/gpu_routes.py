@@ -13,9 +13,11 @@ import torch
 
 from .. import _lib
 
-# Tile heights of the MFMA grouped GEMM (the reference's (BM, BN) choice,
-# gpu_routes.py:67, becomes a choice of MFMA tile height).
-BM_DEFAULT = 64
+# Tile heights of the MFMA grouped GEMM.  96 rows cover a typical expert
+# (64 +- 8 routes per 2048-token chunk) in one tile, so its weights stream
+# once through the pipelined kernel; the reference's large_tile switch
+# (gpu_routes.py:67) selects 128-row tiles (register-prefetch kernel).
+BM_DEFAULT = 96
 BM_LARGE = 128
 
 
