@@ -184,55 +184,142 @@ __device__ __forceinline__ unsigned long long topk_key(float v, int idx) {
 __device__ __forceinline__ int topk_key_index(unsigned long long k) {
   return (int)(0xFFFFu - (uint32_t)(k & 0xFFFFu));
 }
+// The logit a key was made from (-0 comes back as +0, which leaves every
+// later use unchanged).
+__device__ __forceinline__ float topk_key_value(unsigned long long k) {
+  const uint32_t b = (uint32_t)(k >> 32);
+  return __uint_as_float((b & 0x80000000u) ? (b & 0x7FFFFFFFu) : ~b);
+}
+
+// 64-bit value moved between lanes by one DPP pattern (both halves).
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long k) {
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)k, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(k >> 32), CTRL, 0xF, 0xF, false);
+  return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+// Maximum over each 16-lane row, in every lane of the row: neighbours in a
+// quad, then quads of a half-row (half mirror), then half-rows (mirror).
+__device__ __forceinline__ unsigned long long row_max_u64(unsigned long long k) {
+  unsigned long long o = dpp_u64<0xB1>(k);
+  k = o > k ? o : k;
+  o = dpp_u64<0x4E>(k);
+  k = o > k ? o : k;
+  o = dpp_u64<0x141>(k);
+  k = o > k ? o : k;
+  o = dpp_u64<0x140>(k);
+  return o > k ? o : k;
+}
+__device__ __forceinline__ float row_sum_f32(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  return v;
+}
+__device__ __forceinline__ unsigned long long readlane_u64(unsigned long long k, int lane) {
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)k, lane);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), lane);
+  return ((unsigned long long)hi << 32) | lo;
+}
+
+// LDS scratch of one top-k wave, in 64-bit words: 4 rows x 16 candidates
+// plus 16 selected probabilities.
+constexpr int kTopkScratch = 80;
 
 // One wave per token.  Selection key: (logit desc, expert id asc).  Softmax
 // over all experts in fp32, renormalised over the selected ones, bf16 out.
+// Lane l holds experts 4 l .. 4 l + 3, so 16-lane row r holds 64 r ..
+// 64 r + 63.  Each row first finds its own top K with DPP maxima (no LDS
+// round trips), then every one of the 4 K row winners takes its rank among
+// all of them from LDS; the K best ranks are the selection.  K <= 16,
+// E <= 256.  The probability sum runs in selection order.
 __device__ __forceinline__ void topk_wave(const float *lg, int E, int K, int lane,
-                                          int64_t *ids_out, uint16_t *w_out) {
+                                          unsigned long long *scratch, int64_t *ids_out,
+                                          uint16_t *w_out) {
   unsigned long long key[4];
   float v[4];
+  if (E == 256) {
+    const float4 f = *reinterpret_cast<const float4 *>(lg + lane * 4);
+    v[0] = f.x;
+    v[1] = f.y;
+    v[2] = f.z;
+    v[3] = f.w;
+  } else {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = lane + 64 * j;
-    v[j] = e < E ? lg[e] : -INFINITY;
-    key[j] = e < E ? topk_key(v[j], e) : 0ull;
+    for (int j = 0; j < 4; ++j) v[j] = lane * 4 + j < E ? lg[lane * 4 + j] : -INFINITY;
   }
-  float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
-  mx = wave_max_f32(mx);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) key[j] = lane * 4 + j < E ? topk_key(v[j], lane * 4 + j) : 0ull;
+  auto cswap = [&](int a, int b) {
+    if (key[a] < key[b]) {
+      const unsigned long long tmp = key[a];
+      key[a] = key[b];
+      key[b] = tmp;
+    }
+  };
+  cswap(0, 1);
+  cswap(2, 3);
+  cswap(0, 2);
+  cswap(1, 3);
+  cswap(1, 2);
+  // Row-local top K: the lane holding a row's maximum pops it.
+  unsigned long long top[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    top[i] = 0ull;
+    if (i < K) {
+      const unsigned long long m = row_max_u64(key[0]);
+      top[i] = m;
+      if (key[0] == m) {
+        key[0] = key[1];
+        key[1] = key[2];
+        key[2] = key[3];
+        key[3] = 0ull;
+      }
+    }
+  }
+  const int row = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (i < K && (lane & 15) == i) scratch[row * K + i] = top[i];
+  // Softmax statistics: the global maximum is the best of the row maxima.
+  unsigned long long mk = readlane_u64(top[0], 0);
+#pragma unroll
+  for (int r = 1; r < 4; ++r) {
+    const unsigned long long o = readlane_u64(top[0], 16 * r);
+    mk = o > mk ? o : mk;
+  }
+  const float mx = topk_key_value(mk);
   float part = 0.0f;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    if (lane + 64 * j < E) part += expf(v[j] - mx);
-  const float denom = wave_sum_f32(part);
-  // Selection: K rounds of a wave-wide max over (value, -id) keys.
-  float p[16];
-  int id[16];
+    if (lane * 4 + j < E) part += expf(v[j] - mx);
+  part = row_sum_f32(part);
+  const float denom = (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 0)) +
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16))) +
+                      (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 32)) +
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 48)));
+  __builtin_amdgcn_wave_barrier();
+  // Rank of each row winner among all 4 K of them (keys are distinct; the
+  // 0 keys of missing experts rank last).
+  const int nc = 4 * K;
+  const unsigned long long mine = lane < nc ? scratch[lane] : 0ull;
+  int rank = 0;
+#pragma unroll 8
+  for (int j = 0; j < nc; ++j) rank += scratch[j] > mine ? 1 : 0;
+  float *prob = reinterpret_cast<float *>(scratch + 64);
+  const bool chosen = lane < nc && rank < K;
+  const float pe = expf(topk_key_value(mine) - mx) / denom;
+  if (chosen) prob[rank] = pe;
+  __builtin_amdgcn_wave_barrier();
   float psum = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if (i < K) {
-      unsigned long long best = key[0];
-#pragma unroll
-      for (int j = 1; j < 4; ++j) best = key[j] > best ? key[j] : best;
-      best = wave_max_u64(best);
-      const int e = topk_key_index(best);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (key[j] == best) key[j] = 0ull;
-      const float pe = expf(lg[e] - mx) / denom;
-      p[i] = pe;
-      id[i] = e;
-      psum += pe;
-    }
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (i < K) {
-        ids_out[i] = id[i];
-        w_out[i] = f32_to_bf16_bits(p[i] / psum);
-      }
-    }
+  for (int i = 0; i < 16; ++i)
+    if (i < K) psum += prob[i];
+  if (chosen) {
+    ids_out[rank] = topk_key_index(mine);
+    w_out[rank] = f32_to_bf16_bits(pe / psum);
   }
 }
 

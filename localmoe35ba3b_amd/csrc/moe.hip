@@ -26,9 +26,10 @@ constexpr int kI = 512;
 constexpr int kE = 256;
 constexpr int kTopK = 8;
 constexpr int kBM = 96;  // prefill MFMA tile height (one tile covers a typical expert)
+static_assert(kE == 256, "the prefill kernels map one thread of a 256-thread workgroup to each expert");
 
 struct WsLayout {
-  int64_t ctr, xn, gl, logits, ids, wts, sel, selw, xq, xs, pos, table, ordered, slots, hbuf,
+  int64_t ctr, bcounts, xn, gl, logits, ids, wts, sel, selw, xq, xs, pos, table, rslot, rpos, hbuf,
       vbuf, total;
   int64_t max_tiles, n_tiles;
 };
@@ -58,8 +59,9 @@ static WsLayout layout(int64_t T) {
   w.xs = take(kH / 128 * 4);
   w.pos = take((R + T) * 8);
   w.table = take(w.n_tiles * 3 * 8);
-  w.ordered = take(R * 8);
-  w.slots = take(R * 8);
+  w.bcounts = take((T + 15) / 16 * kE * 4);  // per top-k workgroup expert counts
+  w.rslot = take(R * 4);  // rank of each route inside its top-k workgroup and expert
+  w.rpos = take(R * 4);   // sorted row of each route
   w.hbuf = take((R + T) * kI * 2);
   w.vbuf = take((R + T) * kH * 2);
   w.total = o;
@@ -209,12 +211,14 @@ __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
 __device__ __forceinline__ void decode_topk(const LayerArgs &a, float *lgs, int *sel, float *selw) {
   __shared__ int64_t sid[kTopK];
   __shared__ uint16_t swt[kTopK];
+  __shared__ unsigned long long scratch[kTopkScratch];
   const int t = threadIdx.x;
   const int lane = t & 63;
   lgs[t] = a.logits[t];
   __syncthreads();
   if (t < 64) {
-    topk_wave(lgs, kE, kTopK, lane, sid, swt);
+    topk_wave(lgs, kE, kTopK, lane, scratch, sid, swt);
+    __builtin_amdgcn_wave_barrier();
     if (lane == 0) {
       int ids[kTopK];
       float w[kTopK];
@@ -265,7 +269,7 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
   __shared__ __align__(16) unsigned char xbuf[kH * 2];
   __shared__ float xs[G];
   __shared__ float term[R * G];
-  __shared__ float lgs[kE];
+  __shared__ __align__(16) float lgs[kE];
   __shared__ int sel[kTopK];
   __shared__ float selw[kTopK];
   const int t = threadIdx.x;
@@ -457,23 +461,192 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a) {
   if (t == 0) a.gl[tok] = round_bf16((float)(dred[0] + dred[1] + dred[2] + dred[3]));
 }
 
+// Top-k of every prefill token (one wave per token, kTopkTokens tokens per
+// workgroup) that also ranks each route among the workgroup's routes to the
+// same expert (LDS atomics) and writes the workgroup's per-expert counts as
+// one row of bcounts [workgroups, kE].  No global atomics: the row of a
+// route in the expert-sorted order is fixed later from column prefixes of
+// bcounts.  Rows of one expert are in no particular order - the grouped
+// GEMMs compute every row independently and the combine walks a token's
+// routes in ascending expert id, so the layer output does not depend on it.
+constexpr int kTopkTokens = 16;
+constexpr int kScanRoutes = 1024;  // routes per prefill_scan_kernel workgroup
+constexpr int kScanGroups = kScanRoutes / (kTopkTokens * kTopK);  // top-k workgroups per scan one
+static_assert(kScanGroups * kTopkTokens * kTopK == kScanRoutes, "scan slices whole top-k groups");
+
+__global__ __launch_bounds__(1024) void prefill_topk_count_kernel(LayerArgs a, int T, int *bcounts,
+                                                                  int *rslot) {
+  __shared__ int lcnt[kE];
+  __shared__ int64_t sid[16][kTopK];
+  __shared__ uint16_t swt[16][kTopK];
+  __shared__ unsigned long long scratch[16][kTopkScratch];
+  static_assert(kTopkTokens == 16, "one wave per token");
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int w = t >> 6;
+  if (t < kE) lcnt[t] = 0;
+  __syncthreads();
+  const int tok = blockIdx.x * kTopkTokens + w;
+  int e = -1, rank = 0;
+  if (tok < T) {  // wave-uniform
+    topk_wave(a.logits + (int64_t)tok * kE, kE, kTopK, lane, scratch[w], sid[w], swt[w]);
+    __builtin_amdgcn_wave_barrier();
+    if (lane < kTopK) {
+      e = (int)sid[w][lane];
+      a.ids[(int64_t)tok * kTopK + lane] = e;
+      a.wts[(int64_t)tok * kTopK + lane] = swt[w][lane];
+      rank = atomicAdd(&lcnt[e], 1);
+    }
+  }
+  __syncthreads();
+  if (t < kE) bcounts[(int64_t)blockIdx.x * kE + t] = lcnt[t];
+  if (e >= 0) rslot[(int64_t)tok * kTopK + lane] = rank;
+}
+
+// Expert offsets and, for each route, its row in the expert-sorted order:
+// offs[e] + (routes to e of earlier top-k workgroups) + rank inside its own
+// workgroup.  Each workgroup handles kScanRoutes routes and sums the bcounts
+// columns itself (nb rows, L2-resident), so no grid-wide step is needed.
+// Workgroup 0 also writes the tile table (kBM-row tiles per expert, surplus
+// rows (0, 0, 0), then the shared expert's tiles over rows [R, R + T)) and
+// the shared rows' tokens.
+__global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__restrict__ ids,
+                                                            const int *__restrict__ rslot,
+                                                            const int *__restrict__ bcounts,
+                                                            int nb, int T, int max_tiles,
+                                                            int64_t *__restrict__ pos,
+                                                            int64_t *__restrict__ table,
+                                                            int *__restrict__ rpos) {
+  __shared__ int ptot[4][kE], ppre[4][kE], bpre[kScanGroups][kE];
+  __shared__ int offs[kE + 1], tends[kE], scratch[4];
+  const int t = threadIdx.x;
+  const int R = T * kTopK;
+  const int r = blockIdx.x * kScanRoutes + t;
+  const int e_r = r < R ? (int)ids[r] : 0;
+  const int s_r = r < R ? rslot[r] : 0;
+  const int j0 = blockIdx.x * kScanGroups;
+  {
+    const int e = t & (kE - 1), q = t >> 8;
+    int tot = 0, pre = 0;
+#pragma unroll 16
+    for (int j = q; j < nb; j += 4) {
+      const int c = bcounts[(int64_t)j * kE + e];
+      tot += c;
+      pre += j < j0 ? c : 0;
+    }
+    ptot[q][e] = tot;
+    ppre[q][e] = pre;
+  }
+  __syncthreads();
+  int c = 0;
+  if (t < kE) {
+    c = ptot[0][t] + ptot[1][t] + ptot[2][t] + ptot[3][t];
+    int p = ppre[0][t] + ppre[1][t] + ppre[2][t] + ppre[3][t];
+#pragma unroll
+    for (int j = 0; j < kScanGroups; ++j) {
+      bpre[j][t] = p;
+      p += (j0 + j < nb) ? bcounts[(int64_t)(j0 + j) * kE + t] : 0;
+    }
+  }
+  auto scan = [&](int v, int *total) {
+    const int ln = t & 63, wave = t >> 6;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o, 64);
+      if (ln >= o) incl += u;
+    }
+    if (ln == 63 && wave < 4) scratch[wave] = incl;
+    __syncthreads();
+    int base = 0;
+    for (int i = 0; i < wave && i < 4; ++i) base += scratch[i];
+    *total = scratch[0] + scratch[1] + scratch[2] + scratch[3];
+    __syncthreads();
+    return base + incl - v;
+  };
+  int all = 0;
+  const int ex = scan(c, &all);
+  if (t < kE) offs[t] = ex;
+  if (t == 0) offs[kE] = all;
+  __syncthreads();
+  if (r < R) {
+    const int jb = r / (kTopkTokens * kTopK) - j0;
+    const int p = offs[e_r] + bpre[jb][e_r] + s_r;
+    pos[p] = r / kTopK;
+    rpos[r] = p;
+  }
+  if (blockIdx.x != 0) return;
+  const int nt = t < kE ? (c + kBM - 1) / kBM : 0;
+  int ntot = 0;
+  const int tex = scan(nt, &ntot);
+  if (t < kE) tends[t] = tex + nt;
+  __syncthreads();
+  for (int i = t; i < max_tiles; i += 1024) {
+    int64_t te = 0, ts = 0, tp = 0;
+    if (i < ntot) {
+      int l = 0, h = kE;
+      while (l < h) {
+        const int mid = (l + h) >> 1;
+        if (tends[mid] <= i) l = mid + 1;
+        else h = mid;
+      }
+      const int prior = l > 0 ? tends[l - 1] : 0;
+      te = l;
+      ts = offs[l] + (int64_t)(i - prior) * kBM;
+      tp = offs[l + 1];
+    }
+    table[i * 3] = te;
+    table[i * 3 + 1] = ts;
+    table[i * 3 + 2] = tp;
+  }
+  const int nst = (T + kBM - 1) / kBM;
+  for (int j = t; j < nst; j += 1024) {
+    table[(int64_t)(max_tiles + j) * 3] = kE;
+    table[(int64_t)(max_tiles + j) * 3 + 1] = R + (int64_t)j * kBM;
+    table[(int64_t)(max_tiles + j) * 3 + 2] = R + T;
+  }
+  for (int tok = t; tok < T; tok += 1024) pos[R + tok] = tok;
+}
+
 // Per token: routed combine in ascending expert order, gated shared add,
 // residual add (in place on h).  256 threads x 8 columns.
-__global__ __launch_bounds__(256) void prefill_combine_kernel(LayerArgs a, const int64_t *ordered,
-                                                              const int64_t *slots,
+__global__ __launch_bounds__(256) void prefill_combine_kernel(LayerArgs a, const int *rpos,
                                                               const uint16_t *vbuf, int64_t R) {
   const int tok = blockIdx.x;
   const int c = threadIdx.x * 8;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int e[kTopK], p[kTopK];
+  float w[kTopK];
+#pragma unroll
   for (int i = 0; i < kTopK; ++i) {
-    const int64_t route = ordered[(int64_t)tok * kTopK + i];
-    const int64_t slot = slots[(int64_t)tok * kTopK + i];
-    const float w = bf16_bits_to_f32(a.wts[(int64_t)tok * kTopK + slot]);
-    const u32x4 v = ldg16(vbuf + route * kH + c);
+    e[i] = (int)a.ids[(int64_t)tok * kTopK + i];
+    p[i] = rpos[(int64_t)tok * kTopK + i];
+    w[i] = bf16_bits_to_f32(a.wts[(int64_t)tok * kTopK + i]);
+  }
+#pragma unroll
+  for (int pass = 0; pass < kTopK; ++pass) {  // ascending expert id (ids are distinct)
+#pragma unroll
+    for (int i = pass & 1; i + 1 < kTopK; i += 2) {
+      if (e[i] > e[i + 1]) {
+        const int te = e[i], tp = p[i];
+        const float tw = w[i];
+        e[i] = e[i + 1];
+        p[i] = p[i + 1];
+        w[i] = w[i + 1];
+        e[i + 1] = te;
+        p[i + 1] = tp;
+        w[i + 1] = tw;
+      }
+    }
+  }
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kTopK; ++i) {
+    const u32x4 v = ldg16(vbuf + (int64_t)p[i] * kH + c);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      acc[2 * j] = round_bf16(acc[2 * j] + round_bf16(bf16_bits_to_f32(v[j] & 0xFFFFu) * w));
-      acc[2 * j + 1] = round_bf16(acc[2 * j + 1] + round_bf16(bf16_bits_to_f32(v[j] >> 16) * w));
+      acc[2 * j] = round_bf16(acc[2 * j] + round_bf16(bf16_bits_to_f32(v[j] & 0xFFFFu) * w[i]));
+      acc[2 * j + 1] =
+          round_bf16(acc[2 * j + 1] + round_bf16(bf16_bits_to_f32(v[j] >> 16) * w[i]));
     }
   }
   const float sig = round_bf16(sigmoid_f32(a.gl[tok]));
@@ -587,8 +760,9 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   const int64_t T = tokens, R = T * kTopK;
   int64_t *pos = reinterpret_cast<int64_t *>(ws + w.pos);
   int64_t *table = reinterpret_cast<int64_t *>(ws + w.table);
-  int64_t *ordered = reinterpret_cast<int64_t *>(ws + w.ordered);
-  int64_t *slots = reinterpret_cast<int64_t *>(ws + w.slots);
+  int *bcounts = reinterpret_cast<int *>(ws + w.bcounts);
+  int *rslot = reinterpret_cast<int *>(ws + w.rslot);
+  int *rpos = reinterpret_cast<int *>(ws + w.rpos);
   uint16_t *vbuf = reinterpret_cast<uint16_t *>(ws + w.vbuf);
   if (int rc = mark(0)) return rc;
   prefill_norm_gate_kernel<<<(unsigned)T, 256, 0, st>>>(a);
@@ -596,10 +770,13 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   if (int rc = mark(1)) return rc;
   if (int rc = router_logits(a.xn, a.router_w, a.router_bias, a.logits, T, kE, kH, st)) return rc;
   if (int rc = mark(2)) return rc;
-  if (int rc = router_topk(a.logits, T, kE, kTopK, a.ids, a.wts, st)) return rc;
+  const int nb = (int)cdiv(T, kTopkTokens);
+  prefill_topk_count_kernel<<<nb, 1024, 0, st>>>(a, (int)T, bcounts, rslot);
+  if (int rc = check_launch("prefill_topk_count_kernel")) return rc;
   if (int rc = mark(3)) return rc;
-  if (int rc = route_plan(a.ids, T, kTopK, kE, kBM, pos, table, w.max_tiles, ordered, slots, T, st))
-    return rc;
+  prefill_scan_kernel<<<cdiv(R, kScanRoutes), 1024, 0, st>>>(a.ids, rslot, bcounts, nb, (int)T,
+                                                              (int)w.max_tiles, pos, table, rpos);
+  if (int rc = check_launch("prefill_scan_kernel")) return rc;
   if (int rc = mark(4)) return rc;
   if (int rc = routed_gemm(a.xn, a.gu_q, a.gu_s, pos, table, w.n_tiles, kBM, a.hbuf, 2 * kI, kH,
                            true, true, a.gu_qes, a.gu_ses, kH, st))
@@ -609,7 +786,7 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
                            false, a.dn_qes, a.dn_ses, kI, st))
     return rc;
   if (int rc = mark(6)) return rc;
-  prefill_combine_kernel<<<(unsigned)T, 256, 0, st>>>(a, ordered, slots, vbuf, R);
+  prefill_combine_kernel<<<(unsigned)T, 256, 0, st>>>(a, rpos, vbuf, R);
   if (int rc = check_launch("prefill_combine_kernel")) return rc;
   if (int rc = mark(7)) return rc;
   if (ids_out || weights_out) {

@@ -132,10 +132,12 @@ __global__ __launch_bounds__(256) void router_logits_mfma(const uint16_t *__rest
 __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ logits, int T, int E,
                                                    int K, int64_t *__restrict__ ids,
                                                    uint16_t *__restrict__ weights) {
+  __shared__ unsigned long long scratch[4][kTopkScratch];
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  topk_wave(logits + (int64_t)t * E, E, K, lane, ids + (int64_t)t * K, weights + (int64_t)t * K);
+  topk_wave(logits + (int64_t)t * E, E, K, lane, scratch[threadIdx.x >> 6], ids + (int64_t)t * K,
+            weights + (int64_t)t * K);
 }
 
 int router_logits(const uint16_t *x, const uint16_t *w, const float *bias, float *logits,
