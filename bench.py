@@ -40,18 +40,84 @@ def parse():
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--no-events', action='store_true',
                    help='time whole steps only (no per-phase HIP events)')
+    p.add_argument('--copy-probe', action='store_true',
+                   help='only run a plain streaming kernel over 256 MiB (torch.neg on int32, '
+                        'five launches): the known-size reference for HBM traffic counters')
     return p.parse_args()
+
+
+def copy_probe(dev):
+    n = 64 << 20  # int32 elements: 256 MiB read and 256 MiB written per launch
+    src = torch.ones(n, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({'copy_probe': 'torch.neg int32', 'bytes_read_per_launch': n * 4,
+                      'bytes_written_per_launch': n * 4, 'launches': 5}), flush=True)
 
 
 def log(msg):
     print(f'[bench] {msg}', file=sys.stderr, flush=True)
 
 
+class HipEvent:
+    """Timing-only HIP event created with hipEventDisableSystemFence: its
+    record skips the system-scope cache writeback and invalidation a default
+    event performs, which would otherwise add microseconds to every short
+    kernel it brackets.  `cuda_event` is the raw handle that the library's
+    phase-event argument takes."""
+    _hip = None
+
+    @classmethod
+    def hip(cls):
+        if cls._hip is None:
+            import ctypes
+            try:
+                cls._hip = ctypes.CDLL('libamdhip64.so')
+            except OSError:
+                cls._hip = ctypes.CDLL('/opt/rocm/lib/libamdhip64.so')
+            cls._hip.hipEventCreateWithFlags.argtypes = [ctypes.c_void_p, ctypes.c_uint]
+            cls._hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            cls._hip.hipEventElapsedTime.argtypes = [ctypes.c_void_p, ctypes.c_void_p,
+                                                     ctypes.c_void_p]
+        return cls._hip
+
+    def __init__(self):
+        import ctypes
+        self._ct = ctypes
+        handle = ctypes.c_void_p()
+        if self.hip().hipEventCreateWithFlags(ctypes.byref(handle), 0x20000000):
+            raise RuntimeError('hipEventCreateWithFlags failed')
+        self.cuda_event = handle.value
+
+    def record(self):
+        if self.hip().hipEventRecord(self.cuda_event, torch.cuda.current_stream().cuda_stream):
+            raise RuntimeError('hipEventRecord failed')
+
+    def elapsed_time(self, end):
+        ms = self._ct.c_float()
+        if self.hip().hipEventElapsedTime(self._ct.byref(ms), self.cuda_event, end.cuda_event):
+            raise RuntimeError('hipEventElapsedTime failed')
+        return ms.value
+
+
 def make_events(n):
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-    for e in evs:
-        e.record()  # creates the underlying hipEvent
-    return evs
+    return [HipEvent() for _ in range(n)]
+
+
+def pmc_traffic():
+    """HBM bytes per launch of each kernel from the rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes, already scaled by the copy-kernel calibration, as
+    recorded in profiles/pmc_traffic.txt (lines 'kernel bytes')."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', 'pmc_traffic.txt')
+    table = {}
+    if os.path.exists(path):
+        for line in open(path):
+            parts = line.split()
+            if len(parts) == 2 and not line.startswith('#') and parts[1].isdigit():
+                table[parts[0]] = int(parts[1])
+    return table
 
 
 def prefill_bytes(active, tokens=CHUNK):
@@ -82,17 +148,19 @@ def cpu_baseline(stack, x, dec_in, cores):
     t_chunk_layer = time.perf_counter() - t0
     log(f'cpu prefill sample: {t_chunk_layer:.2f} s')
     del layer0
-    # decode: the experts a token selects per layer (host copies made first)
-    hd = dec_in[0].float().cpu().numpy()
-    hosts, t_dec = [], 0.0
+    # decode: one token through every layer.  Each layer gets the input the
+    # GPU saw at that layer, so routing (bit-exact) selects the same experts
+    # and only those are copied to the host beforehand.
     ids_buf = torch.empty((1, K), dtype=torch.int32, device=x.device)
     hg = dec_in[0].clone()
+    inputs, hosts, t_dec = [], [], 0.0
     for l in range(stack.L):
+        inputs.append(hg.float().cpu().numpy())
         stack.layer_forward(hg, l, ids_buf)
         hosts.append(stack.layer_host(l, experts=ids_buf.cpu().numpy()[0]))
     for l in range(stack.L):
         t0 = time.perf_counter()
-        hd, _ = O.moe_layer(hd, hosts[l], k=K, eps=EPS)
+        O.moe_layer(inputs[l], hosts[l], k=K, eps=EPS)
         t_dec += time.perf_counter() - t0
     prefill_tok_s = CHUNK / (t_chunk_layer * stack.L)
     return {
@@ -115,6 +183,9 @@ def main():
     from localmoe35ba3b_amd.runtime.stack import SyntheticMoEStack
 
     dev = torch.device('cuda:0')
+    if args.copy_probe:
+        copy_probe(dev)
+        return
     t_build = time.perf_counter()
     stack = SyntheticMoEStack(layers=args.layers, seed=4, device=dev, max_tokens=CHUNK)
     torch.cuda.synchronize()
@@ -137,6 +208,21 @@ def main():
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         stack.forward(static)
+    # Per-kernel decode times: ROCm graphs cannot hold event records, so each
+    # timed request ends with one more decode token launched eagerly with HIP
+    # events between its kernels.  A spin kernel placed in front holds the
+    # stream until all 40 layers are queued, so the events see the kernels
+    # back to back, as in the graph, not the host's launch gaps.  That token
+    # is timed apart from the 33 graph-replayed tokens of decode tok/s.
+    dec_ev = None if args.no_events else [make_events(4) for _ in range(L)]
+    spin_cycles = 0
+    if dec_ev is not None:
+        a, b = make_events(2)
+        a.record()
+        torch.cuda._sleep(1 << 20)
+        b.record()
+        torch.cuda.synchronize()
+        spin_cycles = int((1 << 20) * 3.0 / max(a.elapsed_time(b), 1e-3))  # ~3 ms
 
     pf_events = None if args.no_events else [[make_events(8) for _ in range(L)]
                                              for _ in range(nchunks)]
@@ -154,6 +240,12 @@ def main():
             static.copy_(dec_in[i])
             graph.replay()
 
+    def decode_kernel_probe():
+        static.copy_(dec_in[-1])
+        torch.cuda._sleep(spin_cycles)
+        for l in range(L):
+            stack.layer_forward(static, l, events=dec_ev[l])
+
     for _ in range(args.warmup):
         prefill()
         decode()
@@ -162,6 +254,7 @@ def main():
 
     marks = [make_events(3) for _ in range(args.steps)]
     phase_ms = {p: 0.0 for p in PREFILL_PHASES}
+    dec_ms = {p: 0.0 for p in DECODE_PHASES}
     t_prefill = t_decode = 0.0
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
@@ -172,6 +265,8 @@ def main():
         m[1].record()
         decode()
         m[2].record()
+        if dec_ev is not None:
+            decode_kernel_probe()
         if pf_events is not None:
             torch.cuda.synchronize()
             for c in range(nchunks):
@@ -179,6 +274,9 @@ def main():
                     ev = pf_events[c][l]
                     for i, p in enumerate(PREFILL_PHASES):
                         phase_ms[p] += ev[i].elapsed_time(ev[i + 1])
+            for l in range(L):
+                for j, p in enumerate(DECODE_PHASES):
+                    dec_ms[p] += dec_ev[l][j].elapsed_time(dec_ev[l][j + 1])
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     for m in marks:
@@ -190,8 +288,7 @@ def main():
     decode_tok_s = steps * DECODE_TOKENS / t_decode
     decode_gbs = DECODE_LAYER_BYTES * L * decode_tok_s / 1e9
 
-    # untimed: routing statistics (active experts per layer-chunk) and the
-    # per-kernel decode times of one eager (non-graph) request
+    # untimed: routing statistics (active experts per layer-chunk)
     ids = torch.empty((CHUNK, K), dtype=torch.int32, device=dev)
     active = []
     out = x.clone()
@@ -200,17 +297,6 @@ def main():
         for l in range(L):
             stack.layer_forward(hc, l, ids)
             active.append(int(torch.unique(ids).numel()))
-    dec_ev = [make_events(4) for _ in range(L)]
-    dec_ms = {p: 0.0 for p in DECODE_PHASES}
-    hd = static.clone()
-    for i in range(DECODE_TOKENS):
-        hd.copy_(dec_in[i])
-        for l in range(L):
-            stack.layer_forward(hd, l, events=dec_ev[l])
-        torch.cuda.synchronize()
-        for l in range(L):
-            for j, p in enumerate(DECODE_PHASES):
-                dec_ms[p] += dec_ev[l][j].elapsed_time(dec_ev[l][j + 1])
 
     launches_pf = steps * nchunks * L
     mean_active = float(np.mean(active))
@@ -229,16 +315,17 @@ def main():
         for p in ('norm_gate', 'router_logits', 'topk', 'route_plan', 'combine'):
             kernels['prefill_' + p] = {'avg_us': round(phase_ms[p] / launches_pf * 1e3, 2),
                                        'total_ms': round(phase_ms[p], 3)}
-    n_dec = DECODE_TOKENS * L
+    n_dec = steps * L  # decode launches timed: the probe token of every request
     dec_bytes = {'decode_router': E * H * 2 + H * 2,
                  'decode_gate_up': 9 * GU_EXPERT_BYTES,
                  'decode_down': 9 * DN_EXPERT_BYTES}
-    for p in DECODE_PHASES:
-        avg_us = dec_ms[p] / n_dec * 1e3
-        kernels[p] = {'avg_us': round(avg_us, 2), 'launches': n_dec,
-                      'bytes_per_launch': dec_bytes[p],
-                      'gbs': round(dec_bytes[p] / avg_us / 1e3, 1),
-                      'total_ms_per_request': round(dec_ms[p], 3)}
+    if dec_ev is not None:
+        for p in DECODE_PHASES:
+            avg_us = dec_ms[p] / n_dec * 1e3
+            kernels[p] = {'avg_us': round(avg_us, 2), 'launches': n_dec,
+                          'bytes_per_launch': dec_bytes[p],
+                          'gbs': round(dec_bytes[p] / avg_us / 1e3, 1),
+                          'ms_per_request': round(avg_us * L * DECODE_TOKENS / 1e3, 3)}
 
     # dominant kernel by total time within one request
     per_req = {}
@@ -246,19 +333,18 @@ def main():
         per_req['prefill_gate_up'] = phase_ms['gate_up'] / steps
         per_req['prefill_down'] = phase_ms['down'] / steps
         per_req['prefill_router_logits'] = phase_ms['router_logits'] / steps
-    for p in DECODE_PHASES:
-        per_req[p] = dec_ms[p]
-    dom = max(per_req, key=per_req.get)
+        for p in DECODE_PHASES:
+            per_req[p] = dec_ms[p] / steps * DECODE_TOKENS
     roofline = None
-    if 'bytes_per_launch' in kernels.get(dom, {}):
+    if per_req:
+        dom = max(per_req, key=per_req.get)
         k = kernels[dom]
         achieved = k['bytes_per_launch'] / k['avg_us'] / 1e3
         roofline = {'bound': 'hbm', 'kernel': dom, 'achieved': round(achieved, 1),
                     'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4),
-                    'traffic': None, 'bytes_per_launch': k['bytes_per_launch'],
+                    'traffic': pmc_traffic().get(dom), 'bytes_per_launch': k['bytes_per_launch'],
                     'avg_us': k['avg_us']}
 
-    log('per-kernel decode timing done')
     cores = min(16, os.cpu_count() or 1)
     cpu = None if args.no_cpu_baseline else cpu_baseline(stack, x, dec_in, cores)
 

@@ -741,7 +741,9 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   auto mark = [&](int i) -> int {
     if (!phase_events) return LM_OK;
     hipError_t e = hipEventRecord(static_cast<hipEvent_t>(phase_events[i]), st);
-    return e == hipSuccess ? LM_OK : set_error(LM_ELAUNCH, "hipEventRecord failed");
+    return e == hipSuccess ? LM_OK
+                           : set_error(LM_ELAUNCH, std::string("hipEventRecord failed: ") +
+                                                       hipGetErrorString(e));
   };
 
   if (tokens == 1) {
