@@ -5,17 +5,19 @@
 // Decode (one token) runs three kernels and never leaves the device:
 //   decode_router_kernel   RMSNorm, fp64 router logits (one wave per expert),
 //                          activation quantization of the normalized row, the
-//                          shared-expert gate; the last workgroup to finish
-//                          runs top-8 + softmax renormalisation.
-//   decode_gate_up_kernel  gate_up rows of the 8 routed experts (W8A8,
-//                          w8a8.py) and of the shared expert (W8A16), SwiGLU.
+//                          shared-expert gate.
+//   decode_gate_up_kernel  top-8 + softmax renormalisation (every workgroup,
+//                          redundantly), then gate_up rows of the 8 routed
+//                          experts (W8A8, w8a8.py) and of the shared expert
+//                          (W8A16), SwiGLU.
 //   decode_down_kernel     down rows of all 9 experts for 8 output columns,
 //                          W8A8 (row-quantized SwiGLU output) / W8A16, then the
 //                          ascending-expert bf16 combine (int8.py:240-250), the
 //                          gated shared add and the residual add, in place.
-// Prefill runs: RMSNorm + shared gate, router (fp64 MFMA), top-k, device route
-// plan (with the shared expert appended as extra tiles), grouped W8A16 gate_up
-// GEMM with fused SwiGLU, grouped W8A16 down GEMM, and a per-token combine.
+// Prefill runs: RMSNorm + shared gate, router (fp64 MFMA), top-k with
+// per-workgroup expert counts, the route plan scan (with the shared expert
+// appended as extra tiles), grouped W8A16 gate_up GEMM with fused SwiGLU,
+// grouped W8A16 down GEMM, and a per-token combine.
 #include "gemv_core.hpp"
 #include "internal.hpp"
 
