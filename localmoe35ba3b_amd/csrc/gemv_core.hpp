@@ -75,23 +75,19 @@ __device__ __forceinline__ void stream_rows(int R, int G, RowPtr row_ptr, Body b
 // One-batch form of stream_rows for kernels whose waves own at most LOADS
 // instructions: issue() starts every load of the wave, consume() runs the
 // body afterwards, so a prologue placed between the two overlaps the HBM
-// latency.
+// latency.  Every lane issues exactly LOADS loads without branches: slots
+// past the end read pair 0 again (a valid address) and are flagged !ok.
+// All lanes of an octet share one (row, group) pair and hence one ok flag.
+// Branch-free issue keeps the compiler's wait counts exact, so code that
+// needs only older loads does not wait for these.
 template <int LOADS>
 struct RowLoads {
   u32x4 w[LOADS];
-  float s[LOADS];  // per-load group scale (issue_scaled only)
   int r[LOADS], g[LOADS], f[LOADS];
   bool ok[LOADS];
 
   template <typename RowPtr>
   __device__ __forceinline__ void issue(int R, int G, RowPtr row_ptr) {
-    issue_scaled(R, G, row_ptr, [](int) -> const float * { return nullptr; });
-  }
-
-  // Also loads the fp32 scale of each (row, group) next to its weights, so
-  // no second round trip is needed for the scales.
-  template <typename RowPtr, typename ScalePtr>
-  __device__ __forceinline__ void issue_scaled(int R, int G, RowPtr row_ptr, ScalePtr scale_ptr) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nwaves = blockDim.x >> 6;
@@ -107,12 +103,10 @@ struct RowLoads {
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) {
       ok[u] = (ibeg + u < iend) && (ff < total);
-      r[u] = rr;
-      g[u] = gg;
-      f[u] = ff;
-      w[u] = ok[u] ? ldg16(row_ptr(rr) + gg * 128 + sub * 16) : u32x4{0u, 0u, 0u, 0u};
-      const float *sp = scale_ptr(rr);
-      s[u] = (ok[u] && sp) ? sp[gg] : 0.0f;
+      r[u] = ok[u] ? rr : 0;
+      g[u] = ok[u] ? gg : 0;
+      f[u] = ok[u] ? ff : 0;
+      w[u] = ldg16(row_ptr(r[u]) + g[u] * 128 + sub * 16);
       ff += 8;
       gg += 8;
       while (gg >= G) {
@@ -126,13 +120,6 @@ struct RowLoads {
   __device__ __forceinline__ void consume(Body body) {
 #pragma unroll
     for (int u = 0; u < LOADS; ++u) body(w[u], r[u], g[u], f[u], ok[u]);
-  }
-
-  // body(w, scale, r, g, f, ok)
-  template <typename Body>
-  __device__ __forceinline__ void consume_scaled(Body body) {
-#pragma unroll
-    for (int u = 0; u < LOADS; ++u) body(w[u], s[u], r[u], g[u], f[u], ok[u]);
   }
 };
 

@@ -144,8 +144,10 @@ __device__ __forceinline__ double dot_lds_f64(const float *xf, const uint16_t *w
 
 // Router logits of the decode token: blocks 0..E/4-1 take one expert per
 // wave (the router row is loaded before the RMSNorm so its HBM latency
-// overlaps the norm); block E/4 writes the normalized row, its W8A8
-// quantization and the shared-expert gate logit.  No inter-block sync.
+// overlaps the norm); block E/4 computes the shared-expert gate logit.
+// Every block normalizes the row itself, so blocks 0..H/128-1 also write one
+// 128-wide group of the normalized row and its W8A8 quantization (no block
+// carries a serial tail).  No inter-block sync.
 __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
   __shared__ float xf[kH];
   __shared__ float red[4];
@@ -159,6 +161,29 @@ __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
 #pragma unroll
   for (int j = 0; j < kH / 512; ++j) wv[j] = ldg16(wrow + lane * 8 + j * 512);
   norm_row_to_lds(a.h, a.norm_w, a.eps, xf, red);
+
+  if (blockIdx.x < kH / 128) {
+    const int g = blockIdx.x;
+    if (t < 64) {
+      a.xn[g * 128 + 2 * t] = f32_to_bf16_bits(xf[g * 128 + 2 * t]);
+      a.xn[g * 128 + 2 * t + 1] = f32_to_bf16_bits(xf[g * 128 + 2 * t + 1]);
+    } else if (t < 96) {  // w8a8.quantize of group g: 32 lanes x 4 values
+      const int l = t - 64;
+      float v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = xf[g * 128 + l * 4 + j];
+      float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+      const float sc = fmaxf(am, 1e-10f) * (float)(1.0 / 127.0);
+      uint32_t packed = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[j] / sc)) << (8 * j);
+      *reinterpret_cast<uint32_t *>(a.xq + g * 128 + l * 4) = packed;
+      if (l == 0) a.xs[g] = sc;
+    }
+  }
 
   if (routed || wave == 0) {
     double acc = 0.0;
@@ -184,76 +209,36 @@ __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
       }
     }
   }
-  if (!routed) {
-    for (int i = t; i < kH; i += 256) a.xn[i] = f32_to_bf16_bits(xf[i]);
-    const int half = t >> 5, l = t & 31;
-    const float inv127 = (float)(1.0 / 127.0);
-    for (int g = half; g < kH / 128; g += 8) {
-      float v[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = xf[g * 128 + l * 4 + j];
-      float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
-      const float sc = fmaxf(am, 1e-10f) * inv127;
-      uint32_t packed = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[j] / sc)) << (8 * j);
-      *reinterpret_cast<uint32_t *>(a.xq + g * 128 + l * 4) = packed;
-      if (l == 0) a.xs[g] = sc;
-    }
-  }
 }
 
 // Top-8 of the decode token from the router logits (one wave), ascending
 // expert order for the combine.  Every decode gate_up workgroup runs it on
 // the same inputs, so all of them agree bit for bit; workgroup (0, 0)
 // publishes the result for the down kernel and the caller.
-__device__ __forceinline__ void decode_topk(const LayerArgs &a, float *lgs, int *sel, float *selw) {
+__device__ __forceinline__ void decode_topk(const LayerArgs &a, int *sel, float *selw) {
   __shared__ int64_t sid[kTopK];
   __shared__ uint16_t swt[kTopK];
   __shared__ unsigned long long scratch[kTopkScratch];
   const int t = threadIdx.x;
-  const int lane = t & 63;
-  lgs[t] = a.logits[t];
-  __syncthreads();
   if (t < 64) {
-    topk_wave(lgs, kE, kTopK, lane, scratch, sid, swt);
+    topk_wave(a.logits, kE, kTopK, t, scratch, sid, swt);
     __builtin_amdgcn_wave_barrier();
-    if (lane == 0) {
-      int ids[kTopK];
-      float w[kTopK];
-      const bool pub = blockIdx.x == 0 && blockIdx.y == 0;
-      for (int i = 0; i < kTopK; ++i) {
-        ids[i] = (int)sid[i];
-        w[i] = bf16_bits_to_f32(swt[i]);
-        if (pub) {
-          a.ids[i] = sid[i];
-          a.wts[i] = swt[i];
-          if (a.ids_out) a.ids_out[i] = ids[i];
-          if (a.wts_out) a.wts_out[i] = swt[i];
-        }
-      }
-      for (int i = 1; i < kTopK; ++i) {
-        const int ki = ids[i];
-        const float wi = w[i];
-        int m = i - 1;
-        while (m >= 0 && ids[m] > ki) {
-          ids[m + 1] = ids[m];
-          w[m + 1] = w[m];
-          --m;
-        }
-        ids[m + 1] = ki;
-        w[m + 1] = wi;
-      }
-      for (int i = 0; i < kTopK; ++i) {
-        sel[i] = ids[i];
-        selw[i] = w[i];
-        if (pub) {
-          a.sel[i] = ids[i];
-          a.selw[i] = w[i];
-        }
+    if (t < kTopK) {  // route t: its rank among the (distinct) ids is its combine slot
+      const int64_t id = sid[t];
+      const uint16_t wb = swt[t];
+      int rank = 0;
+#pragma unroll
+      for (int j = 0; j < kTopK; ++j) rank += sid[j] < id ? 1 : 0;
+      const float w = bf16_bits_to_f32(wb);
+      sel[rank] = (int)id;
+      selw[rank] = w;
+      if (blockIdx.x == 0 && blockIdx.y == 0) {
+        a.ids[t] = id;
+        a.wts[t] = wb;
+        if (a.ids_out) a.ids_out[t] = (int)id;
+        if (a.wts_out) a.wts_out[t] = wb;
+        a.sel[rank] = (int)id;
+        a.selw[rank] = w;
       }
     }
   }
@@ -268,10 +253,11 @@ constexpr int kGuPairs = 8;
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
   constexpr int G = kH / 128;
   constexpr int R = 2 * kGuPairs;
+  static_assert(R * G == 256, "one group scale per thread");
   __shared__ __align__(16) unsigned char xbuf[kH * 2];
   __shared__ float xs[G];
+  __shared__ float wsc[R * G];
   __shared__ float term[R * G];
-  __shared__ __align__(16) float lgs[kE];
   __shared__ int sel[kTopK];
   __shared__ float selw[kTopK];
   const int t = threadIdx.x;
@@ -279,31 +265,47 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
   const bool shared = slot == kTopK;
   const int n0 = blockIdx.x * kGuPairs;
   const RowMap map{n0, kI + n0, kGuPairs};
+  // Weights stream straight into registers; the block's 256 group scales
+  // come in as one dword per thread, so every in-flight load slot of a lane
+  // but one carries 16 weight bytes.
   RowLoads<8> L;
+  float my_scale = 0.0f;
   auto issue = [&](int e) {
     const int8_t *wq = a.gu_q + (int64_t)e * a.gu_qes;
-    const float *ws = a.gu_s + (int64_t)e * a.gu_ses;
-    L.issue_scaled(
-        R, G, [&](int r) { return wq + (int64_t)map(r) * kH; },
-        [&](int r) { return ws + (int64_t)map(r) * G; });
+    my_scale = a.gu_s[(int64_t)e * a.gu_ses + (int64_t)map(t / G) * G + t % G];
+    L.issue(R, G, [&](int r) { return wq + (int64_t)map(r) * kH; });
   };
-  if (shared) issue(kE);  // independent of the routing: start at once
-  decode_topk(a, lgs, sel, selw);
-  if (!shared) issue(sel[slot]);
+  // Everything that does not depend on the routing is requested before the
+  // top-k: the shared slot's weights and every slot's activation row (kept
+  // in registers until the top-k is done).
+  u32x4 xv = u32x4{0u, 0u, 0u, 0u};
+  float xsv = 0.0f;
   if (shared) {
-    reinterpret_cast<u32x4 *>(xbuf)[t] = ldg16(a.xn + t * 8);
+    xv = ldg16(a.xn + t * 8);
+    issue(kE);
   } else {
-    if (t < kH / 16) reinterpret_cast<u32x4 *>(xbuf)[t] = ldg16(a.xq + t * 16);
-    if (t < G) xs[t] = a.xs[t];
+    if (t < kH / 16) xv = ldg16(a.xq + t * 16);
+    if (t < G) xsv = a.xs[t];
   }
+  if (!shared) {
+    decode_topk(a, sel, selw);
+    issue(sel[slot]);
+  }
+  if (shared) {
+    reinterpret_cast<u32x4 *>(xbuf)[t] = xv;
+  } else {
+    if (t < kH / 16) reinterpret_cast<u32x4 *>(xbuf)[t] = xv;
+    if (t < G) xs[t] = xsv;
+  }
+  wsc[t] = my_scale;
   __syncthreads();
 
   const int sub = t & 7;
   if (shared) {
     const uint16_t *x16 = reinterpret_cast<const uint16_t *>(xbuf);
-    L.consume_scaled([&](u32x4 w, float sc, int r, int g, int f, bool ok) {
+    L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
       uint32_t wd[8];
-      dequant16<BF16>(w, sc, wd);
+      dequant16<BF16>(w, wsc[f], wd);
       const uint16_t *xp = x16 + g * 128 + sub * 16;
       const float p = octet_sum_f32(dot16_w16<BF16>(wd, *reinterpret_cast<const u32x4 *>(xp),
                                                     *reinterpret_cast<const u32x4 *>(xp + 8)));
@@ -311,10 +313,10 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
     });
   } else {
     const int8_t *x8 = reinterpret_cast<const int8_t *>(xbuf);
-    L.consume_scaled([&](u32x4 w, float sc, int r, int g, int f, bool ok) {
+    L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
       const int p = octet_sum_i32(
           dot16_i8(w, *reinterpret_cast<const u32x4 *>(x8 + g * 128 + sub * 16)));
-      if (ok && sub == 0) term[f] = mul_rn(mul_rn((float)p, xs[g]), sc);
+      if (ok && sub == 0) term[f] = mul_rn(mul_rn((float)p, xs[g]), wsc[f]);
     });
   }
   __syncthreads();
@@ -340,6 +342,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   __shared__ float xs[kTopK * G];
   __shared__ __align__(16) uint16_t xsh[kI];
   __shared__ float term[R * G];
+  __shared__ float wsc[R * G];
   __shared__ float selw[kTopK];
   const int t = threadIdx.x;
   const int c0 = blockIdx.x * kDnCols;
@@ -355,23 +358,32 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
       if (s == j) e = ex[j];
     return e;
   };
-  RowLoads<12> L;
-  L.issue_scaled(
-      R, G,
-      [&](int r) {
-        return a.dn_q + (int64_t)expert_of(r) * a.dn_qes + (int64_t)(c0 + r % kDnCols) * kI;
-      },
-      [&](int r) {
-        return a.dn_s + (int64_t)expert_of(r) * a.dn_ses + (int64_t)(c0 + r % kDnCols) * G;
-      });
-
-  // Row quantization of hbuf[0..7]: 16 values per thread, a 128-group is
-  // spread over 8 consecutive lanes.
+  // The SwiGLU rows are requested together with the expert ids; the weight
+  // loads follow as soon as the ids arrive.
   const int row = t >> 5, col = (t & 31) * 16;
   const u32x4 h0 = ldg16(a.hbuf + row * kI + col);
   const u32x4 h1 = ldg16(a.hbuf + row * kI + col + 8);
-  if (t < kI / 8) reinterpret_cast<u32x4 *>(xsh)[t] = ldg16(a.hbuf + kTopK * kI + t * 8);
-  if (t < kTopK) selw[t] = a.selw[t];
+  const u32x4 hsh = t < kI / 8 ? ldg16(a.hbuf + kTopK * kI + t * 8) : u32x4{0u, 0u, 0u, 0u};
+  const float wsel = t < kTopK ? a.selw[t] : 0.0f;
+  // the block's R * G group scales (one or two dwords per thread), then the
+  // weights, so the scales are not queued behind them
+  float sv0 = 0.0f, sv1 = 0.0f;
+  {
+    const int f0 = t, f1 = t + 256;
+    sv0 = a.dn_s[(int64_t)expert_of(f0 / G) * a.dn_ses + (int64_t)(c0 + (f0 / G) % kDnCols) * G +
+                 f0 % G];
+    if (f1 < R * G)
+      sv1 = a.dn_s[(int64_t)expert_of(f1 / G) * a.dn_ses +
+                   (int64_t)(c0 + (f1 / G) % kDnCols) * G + f1 % G];
+  }
+  RowLoads<12> L;
+  L.issue(R, G, [&](int r) {
+    return a.dn_q + (int64_t)expert_of(r) * a.dn_qes + (int64_t)(c0 + r % kDnCols) * kI;
+  });
+  __builtin_amdgcn_sched_barrier(0);  // keep the quantization below the weight loads
+
+  // Row quantization of hbuf[0..7]: 16 values per thread, a 128-group is
+  // spread over 8 consecutive lanes.
   float v[16];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -398,10 +410,15 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   }
   *reinterpret_cast<u32x4 *>(xq + row * kI + col) = packed;
   if ((t & 7) == 0) xs[row * G + col / 128] = sc;
+  wsc[t] = sv0;
+  if (t + 256 < R * G) wsc[t + 256] = sv1;
+  if (t < kI / 8) reinterpret_cast<u32x4 *>(xsh)[t] = hsh;
+  if (t < kTopK) selw[t] = wsel;
   __syncthreads();
 
   const int sub = t & 7;
-  L.consume_scaled([&](u32x4 w, float scl, int r, int g, int f, bool ok) {
+  L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
+    const float scl = wsc[f];
     const int s = r / kDnCols;  // uniform across the wave instruction
     if (s < kTopK) {
       const int p = octet_sum_i32(
