@@ -237,6 +237,27 @@ __global__ __launch_bounds__(256) void w8a16_mfma_kernel(GemmArgs a) {
 constexpr int kGBM = 128;
 constexpr int kLDB = kBK + 8;  // int8 bytes per LDS row of the weight tile
 
+// Eight int8 weights -> eight bf16(q * s): the signed byte converts exactly
+// (v_cvt_f32_i32 with a sign-extended byte operand), so q * s is the
+// correctly rounded fp32 product, then RNE to bf16 - bit-identical to
+// dequant8_bf16 with one operation fewer per four weights.
+__device__ __forceinline__ u32x4 dequant8s_bf16(uint2 w, float s) {
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[i] = (float)(int8_t)(w.x >> (8 * i)) * s;
+    f[4 + i] = (float)(int8_t)(w.y >> (8 * i)) * s;
+  }
+  return u32x4{BF16::pack2(f[0], f[1]), BF16::pack2(f[2], f[3]), BF16::pack2(f[4], f[5]),
+               BF16::pack2(f[6], f[7])};
+}
+
+// SiLU for the prefill epilogue from the hardware exp2 and reciprocal
+// (about 2 ulp in fp32); the product is rounded to bf16 right after.
+__device__ __forceinline__ float silu_fast(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+
 __device__ __forceinline__ u32x4 dequant8_bf16(uint2 w, float s) {
   const float n = -128.0f * s;
   float f[8];
@@ -626,6 +647,282 @@ __global__ __launch_bounds__(256, 2) void grouped_lds_kernel(GemmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Register-streamed variant: the int8 weights never touch LDS.  Each wave
+// owns TN columns of the tile and streams its own weight rows straight into
+// registers, BD stages deep (BD - 1 stages of 64 K in flight while one is
+// consumed), dequantizes them exactly in registers and feeds them to the
+// MFMA as the B operand.  Only the activation rows (shared by the four
+// waves) are staged in LDS, in a 3-slot ring loaded through registers one
+// stage ahead of their LDS write.  All loads are ordinary compiler-tracked
+// loads, so every wait the compiler inserts is exact.
+//
+// K order inside a 64-K stage: lane l (quad q = l >> 4) loads 16 consecutive
+// weights k = 16 q .. 16 q + 15 of its column; MFMA step `sub` takes the
+// half 8 sub .. 8 sub + 7.  The A fragment of the same lane and step reads
+// the same k from LDS, so each product pairs the right x and w (a fixed
+// permutation of the summation order inside the stage).
+//
+// A stage in LDS: BM rows x 128 B (64 bf16); 16-byte chunk p of row r is
+// stored at chunk p ^ (r & 7), so the eight rows read by one lane octet hit
+// eight different bank groups.  Scales of the tile are staged once:
+// [BN cols][K / 128] floats.
+constexpr int rb_gcd(int a, int b) { return b == 0 ? a : rb_gcd(b, a % b); }
+
+// One tile with MS live 16-row sub-tiles (rows <= 16 MS).  Instantiated per
+// MS so the inner loop carries no row branches; every load is unconditional
+// (rows past the tile re-read its last row), which keeps the compiler's
+// wait counts exact.  A stage is KS = 64 HL values of K: each lane loads HL
+// 16-byte pieces per column sub-tile (bytes 64 h + 16 q, h < HL), so one
+// lane quad reads 64 HL contiguous bytes of a weight row.  Weights are
+// requested BD - 1 stages ahead, activation rows AD stages ahead (AD - 1
+// stages wait in registers, one more in LDS).
+template <bool SWIGLU, bool GATHER, int K, int BM, int TN, int BD, int HL, int AD, int NW, int MS>
+__device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t start, int rows,
+                                        int nt, unsigned char *smem) {
+  constexpr int KS = 64 * HL;
+  constexpr int KT = K / KS;
+  constexpr int G = K / 128;
+  constexpr int BN = NW * TN;
+  constexpr int NT = NW * 64;              // threads
+  constexpr int NI = TN / 16;
+  constexpr int AR = 3;
+  constexpr int AS = AD - 1;               // activation stages held in registers
+  constexpr int ROWB = KS * 2;             // LDS bytes per activation row per stage
+  constexpr int CPR = ROWB / 16;           // 16-byte chunks per row
+  constexpr int RPL = 1024 / ROWB;         // rows per 1 KB wave-load
+  constexpr int A_STAGE = BM * ROWB;
+  constexpr int A_W = (MS * 16 / RPL + NW - 1) / NW;  // wave-loads per wave covering 16 MS rows
+  constexpr int SC_P = BN * G / 4;            // 16-byte scale pieces of the tile
+  constexpr int SC_W = (SC_P + NT - 1) / NT;
+  constexpr int U = BD / rb_gcd(BD, AS) * AS;   // unroll: both ring indices static
+  static_assert(MS * 16 <= BM && BD >= 2 && AD >= 2 && NW * A_W * RPL <= BM, "shape");
+  float *scl = reinterpret_cast<float *>(smem + AR * A_STAGE);  // [G][BN]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4;
+  const int8_t *wq = a.q + e * a.q_es;
+  const float *wsc = a.s + e * a.s_es;
+  const int half = a.N >> 1;
+  const int n0 = SWIGLU ? nt * (BN / 2) : nt * BN;
+
+  auto wrow = [&](int c) -> int {  // tile column -> weight row, -1 past the end
+    if constexpr (SWIGLU) {
+      const int j = n0 + (c & (BN / 2 - 1));
+      if (j >= half) return -1;
+      return c < BN / 2 ? j : half + j;
+    } else {
+      const int j = n0 + c;
+      return j < a.N ? j : -1;
+    }
+  };
+  auto col_base = [&](int ni) -> int {
+    if constexpr (SWIGLU) {
+      return ni < NI / 2 ? wave * (TN / 2) + ni * 16
+                         : BN / 2 + wave * (TN / 2) + (ni - NI / 2) * 16;
+    } else {
+      return wave * TN + ni * 16;
+    }
+  };
+
+  // Scales of the tile (16-byte piece p: column p / (G/4), groups 4 (p % (G/4)) ..),
+  // requested first; written to LDS transposed ([group][column], so a wave's
+  // 16 column lanes read consecutive words) once the first stages are in flight.
+  u32x4 sreg[SC_W];
+#pragma unroll
+  for (int j = 0; j < SC_W; ++j) {
+    const int piece = (tid + NT * j) % SC_P;
+    const int wr = wrow(piece / (G / 4));
+    sreg[j] = ldg16(wsc + (int64_t)(wr >= 0 ? wr : 0) * G + (piece % (G / 4)) * 4);
+  }
+  // Weight sources: column col_base(ni) + (lane & 15), bytes 16 q (+ 64 h) of each stage.
+  const int8_t *bsrc[NI];
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni) {
+    const int wr = wrow(col_base(ni) + (lane & 15));
+    bsrc[ni] = wq + (int64_t)(wr >= 0 ? wr : 0) * K + q * 16;
+  }
+  // Activation sources: wave-load j fills rows RPL (4 j + wave) ..; lane ->
+  // row RPL (4 j + wave) + lane / CPR, LDS chunk lane % CPR, which holds the
+  // logical chunk (lane % CPR) ^ (row & 7).
+  const uint16_t *asrc[A_W];
+#pragma unroll
+  for (int j = 0; j < A_W; ++j) {
+    const int r = RPL * (NW * j + wave) + lane / CPR;
+    const int rr = min(r, rows - 1);
+    const int64_t xr = GATHER ? a.pos[start + rr] : start + rr;
+    asrc[j] = a.x + xr * a.ldx + (((lane % CPR) ^ (r & 7)) * 8);
+  }
+
+  u32x4 breg[BD][NI][HL];
+  u32x4 areg[AS][A_W];
+  auto load_b = [&](int slot, int s) {
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int h = 0; h < HL; ++h) breg[slot][ni][h] = ldg16(bsrc[ni] + s * KS + 64 * h);
+  };
+  auto load_a = [&](int slot, int s) {
+#pragma unroll
+    for (int j = 0; j < A_W; ++j) areg[slot][j] = ldg16(asrc[j] + s * KS);
+  };
+  auto store_a = [&](int slot, int s) {
+    unsigned char *base = smem + (s % AR) * A_STAGE;
+#pragma unroll
+    for (int j = 0; j < A_W; ++j)
+      *reinterpret_cast<u32x4 *>(base + (NW * j + wave) * 1024 + lane * 16) = areg[slot][j];
+  };
+
+  f32x4 acc[MS][NI];
+#pragma unroll
+  for (int mi = 0; mi < MS; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Prologue: A(0) into LDS; A(1 .. AD-1) and B(0 .. BD-2) in flight.
+  load_a(0, 0);
+#pragma unroll
+  for (int s = 0; s < BD - 1; ++s) load_b(s, s);
+#pragma unroll
+  for (int j = 0; j < SC_W; ++j) {
+    const int piece = tid + NT * j;
+    const int c = piece / (G / 4), g0 = 4 * (piece % (G / 4));
+    if (piece < SC_P) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) scl[(g0 + i) * BN + c] = __uint_as_float(sreg[j][i]);
+    }
+  }
+  store_a(0, 0);
+#pragma unroll
+  for (int s = 1; s < AD; ++s)
+    if (s < KT) load_a(s % AS, s);
+
+  // Stage s: publish A(s+1), barrier, request A(s+AD) and B(s+BD-1) (into the
+  // slots freed by the previous stage), then dequantize B(s) and run the MFMAs.
+  auto step = [&](int s, int ub, int ua, bool st_a, bool ld_a, bool ld_b) {
+    if (st_a) store_a(ua, s + 1);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+    barrier_raw();
+    if (ld_a) load_a(ua, s + AD);
+    if (ld_b) load_b((ub + BD - 1) % BD, s + BD - 1);
+    const unsigned char *sa = smem + (s % AR) * A_STAGE;
+    const int g = (s * KS) >> 7;
+    float sc[NI];
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) sc[ni] = scl[g * BN + col_base(ni) + (lane & 15)];
+#pragma unroll
+    for (int h = 0; h < HL; ++h) {
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        u32x4 af[MS];
+#pragma unroll
+        for (int mi = 0; mi < MS; ++mi) {
+          const int r = mi * 16 + (lane & 15);
+          af[mi] = *reinterpret_cast<const u32x4 *>(
+              sa + r * ROWB + (((8 * h + 2 * q + sub) ^ (r & 7)) * 16));
+        }
+        u32x4 bfr[NI];
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni)
+          bfr[ni] = dequant8s_bf16(uint2{breg[ub][ni][h][2 * sub], breg[ub][ni][h][2 * sub + 1]},
+                                   sc[ni]);
+#pragma unroll
+        for (int mi = 0; mi < MS; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < NI; ++ni)
+            acc[mi][ni] = BF16::mfma16x16x32(af[mi], bfr[ni], acc[mi][ni]);
+      }
+    }
+  };
+  // Main loop: every load in range.  The tail (TL >= max(BD - 1, AD) stages,
+  // fully unrolled) issues only the loads that are still in range.
+  constexpr int TLM = BD - 1 > AD ? BD - 1 : AD;
+  constexpr int TL0 = KT % U;
+  constexpr int TL = TL0 >= TLM ? TL0 : TL0 + U * ((TLM - TL0 + U - 1) / U);
+  static_assert(TL <= KT, "stage count");
+  for (int s0 = 0; s0 < KT - TL; s0 += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) step(s0 + u, u % BD, (u + 1) % AS, true, true, true);
+  }
+#pragma unroll
+  for (int v = 0; v < TL; ++v) {
+    const int s = KT - TL + v;
+    step(s, s % BD, (s + 1) % AS, s + 1 < KT, s + AD < KT, s + BD - 1 < KT);
+  }
+
+#pragma unroll
+  for (int mi = 0; mi < MS; ++mi) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int rl = mi * 16 + q * 4 + it;
+      if (rl >= rows) continue;
+      uint16_t *yrow = a.y + (start + rl) * a.ldy;
+      if constexpr (SWIGLU) {
+#pragma unroll
+        for (int ni = 0; ni < NI / 2; ++ni) {
+          const int col = n0 + wave * (TN / 2) + ni * 16 + (lane & 15);
+          if (col < half) {
+            const float gate = round_bf16(acc[mi][ni][it]);
+            const float up = round_bf16(acc[mi][ni + NI / 2][it]);
+            yrow[col] = f32_to_bf16_bits(round_bf16(silu_fast(gate)) * up);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+          const int col = n0 + col_base(ni) + (lane & 15);
+          if (col < a.N) yrow[col] = f32_to_bf16_bits(acc[mi][ni][it]);
+        }
+      }
+    }
+  }
+}
+
+template <bool SWIGLU, bool GATHER, int K, int BM, int TN, int BD, int HL, int AD, int NW, int OCC>
+__global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
+  constexpr int SC_BYTES = NW * TN * (K / 128) * 4;
+  __shared__ __align__(16) unsigned char smem[3 * BM * 128 * HL + SC_BYTES];
+  int mt, nt;
+  if (!xcd_tile(a, mt, nt)) return;
+  const int64_t e = a.table[mt * 3];
+  const int64_t start = a.table[mt * 3 + 1];
+  const int64_t stop = a.table[mt * 3 + 2];
+  if (start >= stop) return;
+  const int rows = (int)min((int64_t)a.tile_rows, stop - start);
+  static_assert(BM == 96, "row-count dispatch below covers 96-row tiles");
+  if (rows > 80)
+    rb_tile<SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 6>(a, e, start, rows, nt, smem);
+  else if (rows > 64)
+    rb_tile<SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 5>(a, e, start, rows, nt, smem);
+  else if (rows > 32)
+    rb_tile<SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 4>(a, e, start, rows, nt, smem);
+  else
+    rb_tile<SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem);
+}
+
+#ifndef LM_RB
+#define LM_RB 1
+#endif
+#ifndef LM_RB_TN
+#define LM_RB_TN 32
+#endif
+#ifndef LM_RB_BD
+#define LM_RB_BD 3
+#endif
+#ifndef LM_RB_HL
+#define LM_RB_HL 1
+#endif
+#ifndef LM_RB_OCC
+#define LM_RB_OCC 3
+#endif
+#ifndef LM_RB_AD
+#define LM_RB_AD 3
+#endif
+#ifndef LM_RB_NW
+#define LM_RB_NW 4
+#endif
+
 #ifndef LM_GROUPED_BN
 #define LM_GROUPED_BN 128
 #endif
@@ -635,10 +932,23 @@ __global__ __launch_bounds__(256, 2) void grouped_lds_kernel(GemmArgs a) {
 
 template <bool SWIGLU, bool GATHER>
 static int launch_grouped(GemmArgs a, unsigned mtiles, hipStream_t st) {
+  if (mtiles == 0) return LM_OK;
+#if LM_RB
+  if (a.tile_rows <= 96 && (a.K == 2048 || a.K == 512)) {
+    constexpr int RBN = LM_RB_NW * LM_RB_TN;
+    a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, RBN / 2) : (int)cdiv(a.N, RBN);
+    a.mt_count = (int)mtiles;
+    const unsigned grid = xcd_grid(a.mt_count, a.nt_count);
+    if (a.K == 2048)
+      grouped_rb_kernel<SWIGLU, GATHER, 2048, 96, LM_RB_TN, LM_RB_BD, LM_RB_HL, LM_RB_AD, LM_RB_NW, LM_RB_OCC><<<grid, LM_RB_NW * 64, 0, st>>>(a);
+    else
+      grouped_rb_kernel<SWIGLU, GATHER, 512, 96, LM_RB_TN, LM_RB_BD, LM_RB_HL, LM_RB_AD, LM_RB_NW, LM_RB_OCC><<<grid, LM_RB_NW * 64, 0, st>>>(a);
+    return check_launch("grouped_rb_kernel");
+  }
+#endif
   constexpr int BN = LM_GROUPED_BN;
   a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, BN / 2) : (int)cdiv(a.N, BN);
   a.mt_count = (int)mtiles;
-  if (mtiles == 0) return LM_OK;
   const unsigned grid = xcd_grid(a.mt_count, a.nt_count);
 #if LM_PIPELINED
   if (a.tile_rows <= LM_PIPE_BM && a.K == 2048) {
