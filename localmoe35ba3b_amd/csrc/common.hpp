@@ -234,21 +234,15 @@ constexpr int kTopkScratch = 80;
 // round trips), then every one of the 4 K row winners takes its rank among
 // all of them from LDS; the K best ranks are the selection.  K <= 16,
 // E <= 256.  The probability sum runs in selection order.
-__device__ __forceinline__ void topk_wave(const float *lg, int E, int K, int lane,
-                                          unsigned long long *scratch, int64_t *ids_out,
-                                          uint16_t *w_out) {
+// topk_wave_v takes lane l's logits of experts 4 l .. 4 l + 3 already loaded
+// (-INFINITY past E); topk_wave loads them from lg.
+__device__ __forceinline__ void topk_wave_v(const float vin[4], int E, int K, int lane,
+                                            unsigned long long *scratch, int64_t *ids_out,
+                                            uint16_t *w_out) {
   unsigned long long key[4];
   float v[4];
-  if (E == 256) {
-    const float4 f = *reinterpret_cast<const float4 *>(lg + lane * 4);
-    v[0] = f.x;
-    v[1] = f.y;
-    v[2] = f.z;
-    v[3] = f.w;
-  } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = lane * 4 + j < E ? lg[lane * 4 + j] : -INFINITY;
-  }
+  for (int j = 0; j < 4; ++j) v[j] = vin[j];
 #pragma unroll
   for (int j = 0; j < 4; ++j) key[j] = lane * 4 + j < E ? topk_key(v[j], lane * 4 + j) : 0ull;
   auto cswap = [&](int a, int b) {
@@ -321,6 +315,23 @@ __device__ __forceinline__ void topk_wave(const float *lg, int E, int K, int lan
     ids_out[rank] = topk_key_index(mine);
     w_out[rank] = f32_to_bf16_bits(pe / psum);
   }
+}
+
+__device__ __forceinline__ void topk_wave(const float *lg, int E, int K, int lane,
+                                          unsigned long long *scratch, int64_t *ids_out,
+                                          uint16_t *w_out) {
+  float v[4];
+  if (E == 256) {
+    const float4 f = *reinterpret_cast<const float4 *>(lg + lane * 4);
+    v[0] = f.x;
+    v[1] = f.y;
+    v[2] = f.z;
+    v[3] = f.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = lane * 4 + j < E ? lg[lane * 4 + j] : -INFINITY;
+  }
+  topk_wave_v(v, E, K, lane, scratch, ids_out, w_out);
 }
 
 }  // namespace lm

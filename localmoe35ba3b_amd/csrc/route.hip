@@ -68,11 +68,17 @@ __global__ __launch_bounds__(256) void router_logits_gemv(const uint16_t *__rest
 // tile 16 tokens x 128 experts, each wave 16 x 32.  Lane quad q supplies
 // k = k0 + 8 q + j at MFMA step j (the same permutation for both operands),
 // so one 16-byte load per operand row feeds 8 MFMA steps.
+template <int D>
 __global__ __launch_bounds__(256) void router_logits_mfma(const uint16_t *__restrict__ x,
                                                           const uint16_t *__restrict__ w,
                                                           const float *__restrict__ bias,
                                                           float *__restrict__ logits, int T,
                                                           int E, int H) {
+  // One wave = 16 tokens x 32 experts; K in 32-wide stages held in a
+  // D-stage register ring (D - 1 stages in flight while one is consumed;
+  // H must be a multiple of 32 D).  Even and odd K-steps accumulate into
+  // separate fp64 tiles, added at the end, so four independent MFMA chains
+  // are in flight.
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int t0 = blockIdx.x * 16;
@@ -83,28 +89,36 @@ __global__ __launch_bounds__(256) void router_logits_mfma(const uint16_t *__rest
   const uint16_t *xa = x + (int64_t)min(t0 + r, T - 1) * H + q * 8;
   const uint16_t *wb0 = w + (int64_t)min(e0 + r, E - 1) * H + q * 8;
   const uint16_t *wb1 = w + (int64_t)min(e0 + 16 + r, E - 1) * H + q * 8;
-  f64x4 acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
-  u32x4 av = ldg16(xa), bv0 = ldg16(wb0), bv1 = ldg16(wb1);
-  for (int k0 = 0; k0 < H; k0 += 32) {
-    u32x4 an, bn0, bn1;
-    if (k0 + 32 < H) {
-      an = ldg16(xa + k0 + 32);
-      bn0 = ldg16(wb0 + k0 + 32);
-      bn1 = ldg16(wb1 + k0 + 32);
-    }
+  f64x4 acc[2][2] = {{{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}},
+                     {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}}};
+  u32x4 ra[D], rb0[D], rb1[D];
+  const int last = H - 32;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t sh = (j & 1) ? 16u : 0u;
-      const double a = (double)bf16_bits_to_f32((av[j >> 1] >> sh) & 0xFFFFu);
-      const double b0 = (double)bf16_bits_to_f32((bv0[j >> 1] >> sh) & 0xFFFFu);
-      const double b1 = (double)bf16_bits_to_f32((bv1[j >> 1] >> sh) & 0xFFFFu);
-      acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b0, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b1, acc1, 0, 0, 0);
-    }
-    if (k0 + 32 < H) {
-      av = an;
-      bv0 = bn0;
-      bv1 = bn1;
+  for (int d = 0; d < D; ++d) {
+    const int k = min(32 * d, last);
+    ra[d] = ldg16(xa + k);
+    rb0[d] = ldg16(wb0 + k);
+    rb1[d] = ldg16(wb1 + k);
+  }
+  for (int k0 = 0; k0 < H; k0 += 32 * D) {
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      const u32x4 av = ra[u], bv0 = rb0[u], bv1 = rb1[u];
+      // refill the slot with the stage D ahead (clamped: past the end the
+      // last stage is re-read and never consumed)
+      const int kn = min(k0 + 32 * (u + D), last);
+      ra[u] = ldg16(xa + kn);
+      rb0[u] = ldg16(wb0 + kn);
+      rb1[u] = ldg16(wb1 + kn);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t sh = (j & 1) ? 16u : 0u;
+        const double a = (double)bf16_bits_to_f32((av[j >> 1] >> sh) & 0xFFFFu);
+        const double b0 = (double)bf16_bits_to_f32((bv0[j >> 1] >> sh) & 0xFFFFu);
+        const double b1 = (double)bf16_bits_to_f32((bv1[j >> 1] >> sh) & 0xFFFFu);
+        acc[j & 1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b0, acc[j & 1][0], 0, 0, 0);
+        acc[j & 1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b1, acc[j & 1][1], 0, 0, 0);
+      }
     }
   }
   // D layout of the f64 16x16x4 MFMA: lane holds column (lane & 15) and
@@ -116,12 +130,12 @@ __global__ __launch_bounds__(256) void router_logits_mfma(const uint16_t *__rest
     if (t >= T) continue;
     const int ea = e0 + r, eb = e0 + 16 + r;
     if (ea < E) {
-      float l = round_bf16((float)acc0[i]);
+      float l = round_bf16((float)(acc[0][0][i] + acc[1][0][i]));
       if (bias) l = l + bias[ea];
       logits[(int64_t)t * E + ea] = l;
     }
     if (eb < E) {
-      float l = round_bf16((float)acc1[i]);
+      float l = round_bf16((float)(acc[0][1][i] + acc[1][1][i]));
       if (bias) l = l + bias[eb];
       logits[(int64_t)t * E + eb] = l;
     }
@@ -149,8 +163,11 @@ int router_logits(const uint16_t *x, const uint16_t *w, const float *bias, float
     else
       router_logits_gemv<8><<<g, 256, 0, st>>>(x, w, bias, logits, (int)T, (int)E, (int)H);
   } else {
-    router_logits_mfma<<<dim3(cdiv(T, 16), cdiv(E, 128)), 256, 0, st>>>(x, w, bias, logits,
-                                                                         (int)T, (int)E, (int)H);
+    const dim3 grid(cdiv(T, 16), cdiv(E, 128));
+    if (H % 128 == 0)
+      router_logits_mfma<4><<<grid, 256, 0, st>>>(x, w, bias, logits, (int)T, (int)E, (int)H);
+    else
+      router_logits_mfma<1><<<grid, 256, 0, st>>>(x, w, bias, logits, (int)T, (int)E, (int)H);
   }
   return check_launch("router_logits");
 }
