@@ -1,4 +1,4 @@
-"""HBM-resident synthetic MoE-FFN stack (40 x [RMSNorm -> MoE block -> residual]).
+"""HBM-resident MoE-FFN stack (L x [RMSNorm -> MoE block -> residual]).
 
 Replaces the reference's CPU-pinned expert bank, 7 GiB slab arena and
 frequency-retention cache (runtime/prefill.py:88-164, runtime/slab_cache.py,
@@ -12,11 +12,13 @@ converted artifact, convert.py:96-97):
   dn_q  int8 [L, E+1, H, I]    dn_s fp32 [L, E+1, H, I/128]
 expert index E is the always-on shared expert (its gate_proj / up_proj rows
 concatenated, exact because scales are per row).  Router weights bf16
-[L, E, H], shared-expert gate bf16 [L, H]; the RMSNorm weight is zero
-(scale 1 + w = 1), as for a freshly initialised Qwen3_5MoeRMSNorm.
+[L, E, H], shared-expert gate bf16 [L, H], optional RMSNorm weights fp32
+[L, H] (post_attention_layernorm, scale 1 + w).
 
-Weights are drawn on the GPU from per-(layer, matrix) seeds, N(0, 0.02) fp32,
-and quantized by the group-128 HIP quantizer.
+SyntheticMoEStack fills the bank with random weights drawn on the GPU from
+per-(layer, matrix) seeds, N(0, 0.02) fp32, quantized by the group-128 HIP
+quantizer, and a zero RMSNorm weight; artifact.stack_from_artifact fills it
+from a converted checkpoint.
 """
 import ctypes
 import math
@@ -47,15 +49,17 @@ def zipf_bias(experts=EXPERTS, s=1.1, seed=3):
     return (logp - logp.mean()).astype(np.float32)
 
 
-class SyntheticMoEStack:
-    """Random-init 35B-A3B-class MoE-FFN stack resident in HBM.
+class MoEStack:
+    """HBM-resident MoE-FFN stack: the int8 bank, router and gate weights of
+    every layer plus the fused-layer workspace.  Subclasses / constructors
+    fill the tensors (random init: SyntheticMoEStack; converted checkpoint:
+    artifact.stack_from_artifact).
 
-    layers/experts may be reduced for tests; the fused layer kernels require
-    hidden 2048, intermediate 512, 256 experts and top-8.
+    layers may be reduced for tests; the fused layer kernels require hidden
+    2048, intermediate 512, 256 experts and top-8.
     """
 
-    def __init__(self, layers=40, seed=4, device='cuda', max_tokens=2048, router_bias=None,
-                 chunk_experts=32):
+    def __init__(self, layers, device='cuda', max_tokens=2048, router_bias=None, norm=False):
         self.L = layers
         self.E, self.H, self.I, self.K = EXPERTS, HIDDEN, INTER, TOP_K
         self.device = torch.device(device)
@@ -70,26 +74,12 @@ class SyntheticMoEStack:
                                 device=dev)
         self.router_w = torch.empty((layers, self.E, self.H), dtype=torch.bfloat16, device=dev)
         self.gate_w = torch.empty((layers, self.H), dtype=torch.bfloat16, device=dev)
+        # RMSNorm weight w of (1 + w); None = zeros, as for a freshly initialised norm
+        self.norm_w = (torch.zeros((layers, self.H), dtype=torch.float32, device=dev)
+                       if norm else None)
         self.router_bias = None
         if router_bias is not None:
             self.router_bias = torch.as_tensor(router_bias, dtype=torch.float32).to(dev)
-        gen = torch.Generator(device=dev)
-        for l in range(layers):
-            gen.manual_seed(matrix_seed(seed, l, 0))
-            self.router_w[l] = (torch.randn((self.E, self.H), generator=gen, device=dev)
-                                * 0.02).to(torch.bfloat16)
-            gen.manual_seed(matrix_seed(seed, l, 1))
-            self.gate_w[l] = (torch.randn(self.H, generator=gen, device=dev) * 0.02).to(
-                torch.bfloat16)
-            for c0 in range(0, E1, chunk_experts):
-                c1 = min(E1, c0 + chunk_experts)
-                gen.manual_seed(matrix_seed(seed, l, 2, c0 // chunk_experts))
-                w = torch.randn((c1 - c0, 2 * self.I, self.H), generator=gen, device=dev) * 0.02
-                self.gu_q[l, c0:c1], self.gu_s[l, c0:c1] = quantize_g128(w)
-                gen.manual_seed(matrix_seed(seed, l, 3, c0 // chunk_experts))
-                w = torch.randn((c1 - c0, self.H, self.I), generator=gen, device=dev) * 0.02
-                self.dn_q[l, c0:c1], self.dn_s[l, c0:c1] = quantize_g128(w)
-                del w
         nbytes = _lib.lib().lm_moe_workspace_bytes(max_tokens, self.H, self.I, self.E, self.K)
         if nbytes < 0:
             raise ValueError('unsupported MoE geometry')
@@ -99,15 +89,17 @@ class SyntheticMoEStack:
 
     # ------------------------------------------------------------------ views
     def bank_bytes(self):
-        return sum(t.numel() * t.element_size() for t in
-                   (self.gu_q, self.gu_s, self.dn_q, self.dn_s, self.router_w, self.gate_w))
+        tensors = [self.gu_q, self.gu_s, self.dn_q, self.dn_s, self.router_w, self.gate_w]
+        if self.norm_w is not None:
+            tensors.append(self.norm_w)
+        return sum(t.numel() * t.element_size() for t in tensors)
 
     def _layer_struct(self, l):
         s = _lib.MoeLayer()
         s.router_w = self.router_w[l].data_ptr()
         s.router_bias = self.router_bias.data_ptr() if self.router_bias is not None else None
         s.shared_gate_w = self.gate_w[l].data_ptr()
-        s.norm_w = None
+        s.norm_w = self.norm_w[l].data_ptr() if self.norm_w is not None else None
         s.gu_q = self.gu_q[l].data_ptr()
         s.gu_s = self.gu_s[l].data_ptr()
         s.dn_q = self.dn_q[l].data_ptr()
@@ -169,4 +161,34 @@ class SyntheticMoEStack:
                     router_bias=None if self.router_bias is None
                     else self.router_bias.cpu().numpy(),
                     shared_gate_w=self.gate_w[l].float().cpu().numpy(),
-                    norm_w=None, **banks)
+                    norm_w=None if self.norm_w is None else self.norm_w[l].cpu().numpy(),
+                    **banks)
+
+
+class SyntheticMoEStack(MoEStack):
+    """Random-init 35B-A3B-class MoE-FFN stack resident in HBM: weights drawn
+    on the GPU from per-(layer, matrix) seeds, N(0, 0.02) fp32, quantized by
+    the group-128 HIP quantizer; RMSNorm weight zero."""
+
+    def __init__(self, layers=40, seed=4, device='cuda', max_tokens=2048, router_bias=None,
+                 chunk_experts=32):
+        super().__init__(layers, device, max_tokens, router_bias)
+        dev = self.device
+        E1 = self.E + 1
+        gen = torch.Generator(device=dev)
+        for l in range(layers):
+            gen.manual_seed(matrix_seed(seed, l, 0))
+            self.router_w[l] = (torch.randn((self.E, self.H), generator=gen, device=dev)
+                                * 0.02).to(torch.bfloat16)
+            gen.manual_seed(matrix_seed(seed, l, 1))
+            self.gate_w[l] = (torch.randn(self.H, generator=gen, device=dev) * 0.02).to(
+                torch.bfloat16)
+            for c0 in range(0, E1, chunk_experts):
+                c1 = min(E1, c0 + chunk_experts)
+                gen.manual_seed(matrix_seed(seed, l, 2, c0 // chunk_experts))
+                w = torch.randn((c1 - c0, 2 * self.I, self.H), generator=gen, device=dev) * 0.02
+                self.gu_q[l, c0:c1], self.gu_s[l, c0:c1] = quantize_g128(w)
+                gen.manual_seed(matrix_seed(seed, l, 3, c0 // chunk_experts))
+                w = torch.randn((c1 - c0, self.H, self.I), generator=gen, device=dev) * 0.02
+                self.dn_q[l, c0:c1], self.dn_s[l, c0:c1] = quantize_g128(w)
+                del w
