@@ -134,6 +134,34 @@ def prefill_flops(tokens=CHUNK):
     return {'gate_up': 2.0 * rows * 2 * I * H, 'down': 2.0 * rows * H * I}
 
 
+LM_HEAD_N = 248320  # vocabulary of the 35B-A3B configuration
+
+
+def lm_head_probe(dev, reps=20):
+    """The lm_head W8A16 GEMV of one decode token: y [1, 248320] =
+    x [1, 2048] . bf16(q * s)^T over a random int8 [248320, 2048] weight with
+    fp32 group-128 scales (the largest dense read of a real decode step, run
+    through int8.linear).  Returns its average time and HBM rate."""
+    from localmoe35ba3b_amd.operators.int8 import linear
+    n, k = LM_HEAD_N, H
+    q = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev)
+    s = torch.rand((n, k // 128), device=dev) * 1e-3 + 1e-5
+    x = torch.randn((1, k), device=dev).to(torch.bfloat16)
+    for _ in range(3):
+        linear(x, q, s)
+    ev = make_events(reps + 1)
+    ev[0].record()
+    for i in range(reps):
+        linear(x, q, s)
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    us = sorted(ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(reps))[reps // 2]
+    nbytes = n * k + n * (k // 128) * 4 + k * 2 + n * 2
+    return {'avg_us': round(us, 2), 'launches': reps, 'bytes_per_launch': nbytes,
+            'gbs': round(nbytes / us / 1e3, 1), 'hbm_frac': round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            'shape': f'[1, {k}] x [{n}, {k}] int8 g128'}
+
+
 def cpu_baseline(stack, x, dec_in, cores):
     """The CPU oracle (dequantize-then-matmul, the reference arithmetic on the
     host) on a bounded sample: one 2048-token prefill chunk through one layer
@@ -344,6 +372,8 @@ def main():
                     'peak': HBM_PEAK_GBS, 'unit': 'GB/s', 'frac': round(achieved / HBM_PEAK_GBS, 4),
                     'traffic': pmc_traffic().get(dom), 'bytes_per_launch': k['bytes_per_launch'],
                     'avg_us': k['avg_us']}
+
+    kernels['lm_head_gemv'] = lm_head_probe(dev)  # after the timed steps, timed on its own
 
     cores = min(16, os.cpu_count() or 1)
     cpu = None if args.no_cpu_baseline else cpu_baseline(stack, x, dec_in, cores)
