@@ -806,6 +806,9 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
     barrier_raw();
     if (ld_a) load_a(ua, s + AD);
     if (ld_b) load_b((ub + BD - 1) % BD, s + BD - 1);
+    // keep the requests at the top of the stage: left to itself the scheduler
+    // sinks them below the MFMAs, which shortens the prefetch by a stage
+    __builtin_amdgcn_sched_barrier(0);
     const unsigned char *sa = smem + (s % AR) * A_STAGE;
     const int g = (s * KS) >> 7;
     float sc[NI];
@@ -917,7 +920,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
 #define LM_RB_OCC 3
 #endif
 #ifndef LM_RB_AD
-#define LM_RB_AD 3
+#define LM_RB_AD 2
 #endif
 #ifndef LM_RB_NW
 #define LM_RB_NW 4
