@@ -1,4 +1,4 @@
-// W8A16 MFMA GEMM for prefill (gfx950, v_mfma_f32_16x16x32_{bf16,f16}).
+// W8A16 MFMA GEMMs for prefill (gfx950, v_mfma_f32_16x16x32_{bf16,f16}).
 //
 // Used three ways:
 //   dense   y = x . dequant(q)^T                 lm_w8a16_linear, m > 8 (int8.py:9-37)
@@ -7,14 +7,18 @@
 //   swiglu  the gate_up variant with bf16(bf16(silu(gate)) * up) fused in the
 //           epilogue                                     (prefill.py:75-78)
 //
-// Block = 256 threads (4 waves), tile BM x 128 columns, K staged 64 at a time.
-// Weights stay int8 until they are written to LDS: each thread dequantizes
-// its 16 int8 weights to T(q * s) exactly (the reference rounds the
-// dequantized weight to the activation dtype before the MMA, int8.py:21),
-// so the MFMA consumes bit-identical operands to the reference's tl.dot.
-// Registers prefetch stage k+1 from HBM while the MFMAs consume stage k.
-// In SwiGLU mode a 128-column tile is 64 gate columns + the matching 64 up
-// columns, split so that every lane holds a gate value and its up partner.
+// Every kernel dequantizes each int8 weight to T(q * s) exactly before the
+// MFMA (the reference rounds the dequantized weight to the activation dtype
+// before the MMA, int8.py:21), so the MFMA consumes bit-identical operands
+// to the reference's tl.dot; only the fp32 summation order differs.
+//   w8a16_mfma_kernel    dense and generic: 256 threads, BM x 128 tile, K in
+//                        64-wide stages, weights dequantized into LDS.
+//   grouped_mfma_kernel  routed, any K, up to 128-row tiles (large_tile).
+//   grouped_rb_kernel    routed, the model's K (2048 gate_up, 512 down) and
+//                        tiles of up to 96 rows: weights streamed straight
+//                        into registers and dequantized there.
+// In SwiGLU mode a tile's columns pair every gate column with its up partner
+// in the same lane.
 #include "internal.hpp"
 
 namespace lm {
@@ -431,221 +435,11 @@ __global__ __launch_bounds__(256) void grouped_mfma_kernel(GemmArgs a) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// Pipelined variant for the model's K (2048 gate_up, 512 down): a ring of
-// kRing LDS stages filled by direct global->LDS loads (global_load_lds_dwordx4,
-// 16 bytes per lane straight into LDS, no registers held), so each workgroup
-// keeps two stages (~48 KB) in flight while it computes the third.  Every wave
-// issues the same fixed number of loads per stage, which lets the
-// consumer wait with a constant s_waitcnt vmcnt.  LDS layout per stage:
-//   A  128 rows x 64 bf16 (128 B/row), 16-byte chunk p of row r holds the
-//      chunk p ^ (r & 7) of the source row
-//   B  128 cols x 64 int8 (64 B/col), chunk p of col c holds chunk
-//      p ^ ((c >> 1) & 3)
-// (the XOR swizzles spread the MFMA fragment reads over the LDS banks).  The
-// tile's scales [128 cols][K/128] are staged once, in the same load batch as
-// the first stages.  Rows of absent 8-row groups still load a valid row (the
-// tile's last) so the per-wave load count stays fixed; they are never read.
-#ifndef LM_PIPE_BM
-#define LM_PIPE_BM 96
-#endif
-#ifndef LM_PIPE_RING
-#define LM_PIPE_RING 2
-#endif
-
-typedef __attribute__((address_space(3))) void *lds_ptr_t;
-typedef const __attribute__((address_space(1))) void *gbl_ptr_t;
-
-// One 16-byte-per-lane global->LDS load: lane i writes LDS bytes
-// [base + 16 i, base + 16 i + 16).  Issued through inline asm so the
-// compiler's wait-count insertion does not treat every later LDS read as
-// depending on it (it cannot tell ring slots apart and would wait for all
-// loads in flight); the kernel waits for its loads explicitly (wait_vmcnt).
-__device__ __forceinline__ void load_lds16(const void *g, void *lds_wave_base) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(lds_ptr_t)lds_wave_base);
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-               :
-               : "s"(base), "v"(g)
-               : "memory", "m0");
-}
-
 // Workgroup barrier without the release/acquire fences of __syncthreads():
-// those would make every wave wait for all of its outstanding global->LDS
-// loads.  Callers wait for exactly the loads they need (wait_vmcnt) first;
-// the memory clobber keeps the compiler from moving LDS accesses across.
+// those would make every wave wait for all of its outstanding global loads.
+// Callers wait for exactly what they need first (the LDS writes); the memory
+// clobber keeps the compiler from moving LDS accesses across.
 __device__ __forceinline__ void barrier_raw() { asm volatile("s_barrier" ::: "memory"); }
-
-// s_waitcnt with only the vector-memory counter constrained.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-template <bool SWIGLU, bool GATHER, int K, int BM, int kRing, int kBN>
-__global__ __launch_bounds__(256, 2) void grouped_lds_kernel(GemmArgs a) {
-  constexpr int kStageB = kBN * kBK;  // int8 weights per stage
-  constexpr int G = K / 128;
-  constexpr int KT = K / kBK;
-  constexpr int TN = kBN / 4;
-  constexpr int MI = BM / 16;
-  constexpr int NI = TN / 16;
-  constexpr int kStageA = BM * kBK * 2;
-  constexpr int kStage = kStageA + kStageB;
-  constexpr int A_INS = kStageA / 1024 / 4;  // A load instructions per wave per stage
-  constexpr int B_INS = kStageB / 1024 / 4;  // (2)
-  constexpr int PER_STAGE = A_INS + B_INS;
-  constexpr int SC_BYTES = kBN * G * 4;
-  constexpr int SC_INS = SC_BYTES >= 4096 ? SC_BYTES / 4096 : 1;  // per wave
-  __shared__ __align__(1024) unsigned char smem[kRing * kStage + SC_BYTES];
-  float *scl = reinterpret_cast<float *>(smem + kRing * kStage);
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
-  int mt, nt;
-  if (!xcd_tile(a, mt, nt)) return;
-  const int64_t e = a.table[mt * 3];
-  const int64_t start = a.table[mt * 3 + 1];
-  const int64_t stop = a.table[mt * 3 + 2];
-  if (start >= stop) return;
-  const int rows = (int)min((int64_t)a.tile_rows, stop - start);
-  const int8_t *wq = a.q + e * a.q_es;
-  const float *wsc = a.s + e * a.s_es;
-  const int half = a.N >> 1;
-  const int n0 = SWIGLU ? nt * (kBN / 2) : nt * kBN;
-
-  auto wrow = [&](int c) -> int {
-    if constexpr (SWIGLU) {
-      const int j = n0 + (c & (kBN / 2 - 1));
-      if (j >= half) return -1;
-      return c < kBN / 2 ? j : half + j;
-    } else {
-      const int j = n0 + c;
-      return j < a.N ? j : -1;
-    }
-  };
-  auto col_base = [&](int ni) -> int {
-    if constexpr (SWIGLU) {
-      return ni < NI / 2 ? wave * (TN / 2) + ni * 16
-                         : kBN / 2 + wave * (TN / 2) + (ni - NI / 2) * 16;
-    } else {
-      return wave * TN + ni * 16;
-    }
-  };
-
-  // Per-lane sources of this wave's load instructions (stage offset k0 added later).
-  const uint16_t *asrc[A_INS];
-#pragma unroll
-  for (int j = 0; j < A_INS; ++j) {
-    const int ins = wave * A_INS + j;
-    const int r = ins * 8 + (lane >> 3);
-    const int rr = min(r, rows - 1);
-    const int64_t xr = GATHER ? a.pos[start + rr] : start + rr;
-    const int chunk = (lane & 7) ^ (r & 7);
-    asrc[j] = a.x + xr * a.ldx + chunk * 8;
-  }
-  const int8_t *bsrc[B_INS];
-#pragma unroll
-  for (int j = 0; j < B_INS; ++j) {
-    const int ins = wave * B_INS + j;
-    const int c = ins * 16 + (lane >> 2);
-    const int wr = wrow(c);
-    const int chunk = (lane & 3) ^ ((c >> 1) & 3);
-    bsrc[j] = wq + (int64_t)(wr >= 0 ? wr : 0) * K + chunk * 16;
-  }
-
-  auto issue_stage = [&](int kt) {
-    unsigned char *base = smem + (kt % kRing) * kStage;
-    const int k0 = kt * kBK;
-#pragma unroll
-    for (int j = 0; j < A_INS; ++j) load_lds16(asrc[j] + k0, base + (wave * A_INS + j) * 1024);
-#pragma unroll
-    for (int j = 0; j < B_INS; ++j)
-      load_lds16(bsrc[j] + k0, base + kStageA + (wave * B_INS + j) * 1024);
-  };
-
-  // Scales of the tile: [128 cols][G] floats.
-#pragma unroll
-  for (int j = 0; j < SC_INS; ++j) {
-    const int ins = (G * 16 >= 256) ? wave * SC_INS + j : (wave % (SC_BYTES / 1024));
-    const int lanes_per_col = G / 4;  // 16-byte pieces per column
-    const int c = (ins * 64 + lane) / lanes_per_col;
-    const int piece = (ins * 64 + lane) % lanes_per_col;
-    const int wr = wrow(c);
-    load_lds16(wsc + (int64_t)(wr >= 0 ? wr : 0) * G + piece * 4,
-               reinterpret_cast<unsigned char *>(scl) + ins * 1024);
-  }
-#pragma unroll
-  for (int s = 0; s < kRing - 1; ++s) issue_stage(s);
-
-  f32x4 acc[MI][NI];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (int kt = 0; kt < KT; ++kt) {
-    if (kt + 1 < KT) wait_vmcnt<PER_STAGE * (kRing - 2)>();
-    else wait_vmcnt<0>();
-    barrier_raw();
-    if (kt + kRing - 1 < KT) issue_stage(kt + kRing - 1);
-    const unsigned char *sa = smem + (kt % kRing) * kStage;
-    const int8_t *sb = reinterpret_cast<const int8_t *>(sa + kStageA);
-    const int g = (kt * kBK) >> 7;
-    float sc[NI];
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) sc[ni] = scl[(col_base(ni) + (lane & 15)) * G + g];
-#pragma unroll
-    for (int ks = 0; ks < kBK / 32; ++ks) {
-      const int q = lane >> 4;
-      u32x4 bfr[NI];
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni) {
-        const int c = col_base(ni) + (lane & 15);
-        const int pos = (ks * 2 + (q >> 1)) ^ ((c >> 1) & 3);
-        bfr[ni] = dequant8_bf16(*reinterpret_cast<const uint2 *>(sb + c * kBK + pos * 16 + (q & 1) * 8),
-                                sc[ni]);
-      }
-#pragma unroll
-      for (int mi = 0; mi < MI; ++mi) {
-        const int r = mi * 16 + (lane & 15);
-        const int pos = (ks * 4 + q) ^ (r & 7);
-        const u32x4 af = *reinterpret_cast<const u32x4 *>(sa + r * 128 + pos * 16);
-#pragma unroll
-        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = BF16::mfma16x16x32(af, bfr[ni], acc[mi][ni]);
-      }
-    }
-  }
-
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi) {
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int rl = mi * 16 + (lane >> 4) * 4 + it;
-      if (rl >= rows) continue;
-      uint16_t *yrow = a.y + (start + rl) * a.ldy;
-      if constexpr (SWIGLU) {
-#pragma unroll
-        for (int ni = 0; ni < NI / 2; ++ni) {
-          const int col = n0 + wave * (TN / 2) + ni * 16 + (lane & 15);
-          if (col < half) {
-            const float gate = round_bf16(acc[mi][ni][it]);
-            const float up = round_bf16(acc[mi][ni + NI / 2][it]);
-            yrow[col] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int ni = 0; ni < NI; ++ni) {
-          const int col = n0 + col_base(ni) + (lane & 15);
-          if (col < a.N) yrow[col] = f32_to_bf16_bits(acc[mi][ni][it]);
-        }
-      }
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Register-streamed variant: the int8 weights never touch LDS.  Each wave
@@ -904,9 +698,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
     rb_tile<SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem);
 }
 
-#ifndef LM_RB
-#define LM_RB 1
-#endif
+// Configuration of grouped_rb_kernel (compile-time; these values were chosen
+// by measurement on the 2048-token prefill chunk): columns per wave, weight
+// ring slots, 64-K pieces per stage, occupancy hint, activation prefetch
+// distance in stages, waves per workgroup.
 #ifndef LM_RB_TN
 #define LM_RB_TN 32
 #endif
@@ -929,40 +724,27 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
 #ifndef LM_GROUPED_BN
 #define LM_GROUPED_BN 128
 #endif
-#ifndef LM_PIPELINED
-#define LM_PIPELINED 1
-#endif
 
 template <bool SWIGLU, bool GATHER>
 static int launch_grouped(GemmArgs a, unsigned mtiles, hipStream_t st) {
   if (mtiles == 0) return LM_OK;
-#if LM_RB
   if (a.tile_rows <= 96 && (a.K == 2048 || a.K == 512)) {
     constexpr int RBN = LM_RB_NW * LM_RB_TN;
     a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, RBN / 2) : (int)cdiv(a.N, RBN);
     a.mt_count = (int)mtiles;
     const unsigned grid = xcd_grid(a.mt_count, a.nt_count);
     if (a.K == 2048)
-      grouped_rb_kernel<SWIGLU, GATHER, 2048, 96, LM_RB_TN, LM_RB_BD, LM_RB_HL, LM_RB_AD, LM_RB_NW, LM_RB_OCC><<<grid, LM_RB_NW * 64, 0, st>>>(a);
+      grouped_rb_kernel<SWIGLU, GATHER, 2048, 96, LM_RB_TN, LM_RB_BD, LM_RB_HL, LM_RB_AD, LM_RB_NW,
+                        LM_RB_OCC><<<grid, LM_RB_NW * 64, 0, st>>>(a);
     else
-      grouped_rb_kernel<SWIGLU, GATHER, 512, 96, LM_RB_TN, LM_RB_BD, LM_RB_HL, LM_RB_AD, LM_RB_NW, LM_RB_OCC><<<grid, LM_RB_NW * 64, 0, st>>>(a);
+      grouped_rb_kernel<SWIGLU, GATHER, 512, 96, LM_RB_TN, LM_RB_BD, LM_RB_HL, LM_RB_AD, LM_RB_NW,
+                        LM_RB_OCC><<<grid, LM_RB_NW * 64, 0, st>>>(a);
     return check_launch("grouped_rb_kernel");
   }
-#endif
   constexpr int BN = LM_GROUPED_BN;
   a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, BN / 2) : (int)cdiv(a.N, BN);
   a.mt_count = (int)mtiles;
   const unsigned grid = xcd_grid(a.mt_count, a.nt_count);
-#if LM_PIPELINED
-  if (a.tile_rows <= LM_PIPE_BM && a.K == 2048) {
-    grouped_lds_kernel<SWIGLU, GATHER, 2048, LM_PIPE_BM, LM_PIPE_RING, BN><<<grid, 256, 0, st>>>(a);
-    return check_launch("grouped_lds_kernel");
-  }
-  if (a.tile_rows <= LM_PIPE_BM && a.K == 512) {
-    grouped_lds_kernel<SWIGLU, GATHER, 512, LM_PIPE_BM, LM_PIPE_RING, BN><<<grid, 256, 0, st>>>(a);
-    return check_launch("grouped_lds_kernel");
-  }
-#endif
   grouped_mfma_kernel<SWIGLU, GATHER, BN><<<grid, 256, 0, st>>>(a);
   return check_launch("grouped_mfma_kernel");
 }
