@@ -162,6 +162,41 @@ def lm_head_probe(dev, reps=20):
             'shape': f'[1, {k}] x [{n}, {k}] int8 g128'}
 
 
+def skewed_prefill_probe(dev, reps=5):
+    """One MoE layer on a 2048-token chunk with the router logits biased by a
+    Zipf(1.1) per-expert offset (runtime.stack.zipf_bias): few hot experts
+    with many rows each, many empty.  Times each phase with HIP events and
+    reports the grouped GEMMs against the bf16 MFMA peak."""
+    from localmoe35ba3b_amd.runtime.stack import SyntheticMoEStack, zipf_bias
+    st = SyntheticMoEStack(layers=1, seed=3, device=dev, max_tokens=CHUNK, router_bias=zipf_bias())
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    x = torch.randn((CHUNK, H), generator=gen, device=dev).to(torch.bfloat16)
+    ids = torch.empty((CHUNK, K), dtype=torch.int32, device=dev)
+    st.layer_forward(x.clone(), 0, ids)
+    torch.cuda.synchronize()
+    counts = np.bincount(ids.cpu().numpy().reshape(-1), minlength=E)
+    active = int((counts > 0).sum())
+    ev = [make_events(8) for _ in range(reps)]
+    for r in range(reps):
+        st.layer_forward(x.clone(), 0, events=ev[r])
+    torch.cuda.synchronize()
+    ms = {p: sorted(ev[r][i].elapsed_time(ev[r][i + 1]) for r in range(reps))[reps // 2]
+          for i, p in enumerate(PREFILL_PHASES)}
+    fl = prefill_flops()
+    pb = prefill_bytes(active)
+    out = {'active_experts': active, 'max_rows': int(counts.max()),
+           'layer_us': round(sum(ms.values()) * 1e3, 2)}
+    for p in ('gate_up', 'down'):
+        us = ms[p] * 1e3
+        out[p] = {'avg_us': round(us, 2), 'tflops': round(fl[p] / us / 1e6, 1),
+                  'mfma_frac': round(fl[p] / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                  'bytes_per_launch': pb[p], 'gbs': round(pb[p] / us / 1e3, 1)}
+    del st
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(stack, x, dec_in, cores):
     """The CPU oracle (dequantize-then-matmul, the reference arithmetic on the
     host) on a bounded sample: one 2048-token prefill chunk through one layer
@@ -374,6 +409,7 @@ def main():
                     'avg_us': k['avg_us']}
 
     kernels['lm_head_gemv'] = lm_head_probe(dev)  # after the timed steps, timed on its own
+    skewed = None if args.no_events else skewed_prefill_probe(dev)
 
     cores = min(16, os.cpu_count() or 1)
     cpu = None if args.no_cpu_baseline else cpu_baseline(stack, x, dec_in, cores)
@@ -397,6 +433,7 @@ def main():
         'mean_active_experts': round(mean_active, 1),
         'roofline': roofline,
         'kernels': kernels,
+        'prefill_zipf_layer': skewed,
         'cpu_baseline': cpu,
         'build_s': round(t_build, 1),
     }
