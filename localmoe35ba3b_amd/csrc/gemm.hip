@@ -458,10 +458,15 @@ __device__ __forceinline__ void barrier_raw() { asm volatile("s_barrier" ::: "me
 // permutation of the summation order inside the stage).
 //
 // A stage in LDS: BM rows x 128 B (64 bf16); 16-byte chunk p of row r is
-// stored at chunk p ^ (r & 7), so the eight rows read by one lane octet hit
-// eight different bank groups.  Scales of the tile are staged once:
-// [BN cols][K / 128] floats.
+// stored at chunk p ^ rb_swz(r).  Scales of the tile are staged once,
+// transposed: [K / 128][BN cols] floats.
 constexpr int rb_gcd(int a, int b) { return b == 0 ? a : rb_gcd(b, a % b); }
+
+// LDS chunk swizzle of activation row r (16-byte chunks, XOR on the low
+// three chunk bits).  Rows r and r + 8 read by one 16-lane phase share
+// (r & 7); folding in bit 3 of r puts them on different chunks, so the 16
+// rows of an A fragment hit 16 different bank groups.
+__device__ __forceinline__ int rb_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // One tile with MS live 16-row sub-tiles (rows <= 16 MS).  Instantiated per
 // MS so the inner loop carries no row branches; every load is unconditional
@@ -546,7 +551,7 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
     const int r = RPL * (NW * j + wave) + lane / CPR;
     const int rr = min(r, rows - 1);
     const int64_t xr = GATHER ? a.pos[start + rr] : start + rr;
-    asrc[j] = a.x + xr * a.ldx + (((lane % CPR) ^ (r & 7)) * 8);
+    asrc[j] = a.x + xr * a.ldx + (((lane % CPR) ^ rb_swz(r)) * 8);
   }
 
   u32x4 breg[BD][NI][HL];
@@ -617,7 +622,7 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
         for (int mi = 0; mi < MS; ++mi) {
           const int r = mi * 16 + (lane & 15);
           af[mi] = *reinterpret_cast<const u32x4 *>(
-              sa + r * ROWB + (((8 * h + 2 * q + sub) ^ (r & 7)) * 16));
+              sa + r * ROWB + (((8 * h + 2 * q + sub) ^ rb_swz(r)) * 16));
         }
         u32x4 bfr[NI];
 #pragma unroll
