@@ -173,54 +173,85 @@ __device__ __forceinline__ float add_rn(float a, float b) { return a + b; }
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Order-preserving key of an fp32 value (-0 folded onto +0) packed with an
-// index so that larger key = (larger value, then smaller index).
-__device__ __forceinline__ unsigned long long topk_key(float v, int idx) {
-  v = v + 0.0f;  // -0 -> +0
-  uint32_t b = __float_as_uint(v);
-  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return ((unsigned long long)b << 32) | (uint32_t)(0xFFFFu - (uint32_t)idx);
+// Order-preserving keys packing a logit with an index so that larger key =
+// (larger value, then smaller index); -0 is folded onto +0 and comes back as
+// +0, which leaves every later use unchanged.  Key64 holds any fp32 value;
+// Key32 holds a value whose low 16 bits are zero (a bf16 value, which is what
+// a router without bias produces) in half the bits, so each step of the
+// selection moves and compares one register instead of two.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t k) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, CTRL, 0xF, 0xF, false);
 }
-__device__ __forceinline__ int topk_key_index(unsigned long long k) {
-  return (int)(0xFFFFu - (uint32_t)(k & 0xFFFFu));
-}
-// The logit a key was made from (-0 comes back as +0, which leaves every
-// later use unchanged).
-__device__ __forceinline__ float topk_key_value(unsigned long long k) {
-  const uint32_t b = (uint32_t)(k >> 32);
-  return __uint_as_float((b & 0x80000000u) ? (b & 0x7FFFFFFFu) : ~b);
-}
-
 // 64-bit value moved between lanes by one DPP pattern (both halves).
 template <int CTRL>
 __device__ __forceinline__ unsigned long long dpp_u64(unsigned long long k) {
-  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)k, CTRL, 0xF, 0xF, false);
-  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(k >> 32), CTRL, 0xF, 0xF, false);
-  return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+  const uint32_t lo = dpp_u32<CTRL>((uint32_t)k);
+  const uint32_t hi = dpp_u32<CTRL>((uint32_t)(k >> 32));
+  return ((unsigned long long)hi << 32) | lo;
 }
 // Maximum over each 16-lane row, in every lane of the row: neighbours in a
 // quad, then quads of a half-row (half mirror), then half-rows (mirror).
-__device__ __forceinline__ unsigned long long row_max_u64(unsigned long long k) {
-  unsigned long long o = dpp_u64<0xB1>(k);
+template <typename T, T (*MOVE0)(T), T (*MOVE1)(T), T (*MOVE2)(T), T (*MOVE3)(T)>
+__device__ __forceinline__ T row_max_keys(T k) {
+  T o = MOVE0(k);
   k = o > k ? o : k;
-  o = dpp_u64<0x4E>(k);
+  o = MOVE1(k);
   k = o > k ? o : k;
-  o = dpp_u64<0x141>(k);
+  o = MOVE2(k);
   k = o > k ? o : k;
-  o = dpp_u64<0x140>(k);
+  o = MOVE3(k);
   return o > k ? o : k;
 }
+
+struct Key64 {
+  using T = unsigned long long;
+  static __device__ __forceinline__ T make(float v, int idx) {
+    uint32_t b = __float_as_uint(v + 0.0f);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((T)b << 32) | (uint32_t)(0xFFFFu - (uint32_t)idx);
+  }
+  static __device__ __forceinline__ int index(T k) { return (int)(0xFFFFu - (uint32_t)(k & 0xFFFFu)); }
+  static __device__ __forceinline__ float value(T k) {
+    const uint32_t b = (uint32_t)(k >> 32);
+    return __uint_as_float((b & 0x80000000u) ? (b & 0x7FFFFFFFu) : ~b);
+  }
+  static __device__ __forceinline__ T row_max(T k) {
+    return row_max_keys<T, dpp_u64<0xB1>, dpp_u64<0x4E>, dpp_u64<0x141>, dpp_u64<0x140>>(k);
+  }
+  static __device__ __forceinline__ T readlane(T k, int lane) {
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)k, lane);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), lane);
+    return ((T)hi << 32) | lo;
+  }
+};
+
+struct Key32 {
+  using T = uint32_t;
+  static __device__ __forceinline__ T make(float v, int idx) {
+    uint32_t b = __float_as_uint(v + 0.0f) >> 16;
+    b = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+    return (b << 16) | (0xFFFFu - (uint32_t)idx);
+  }
+  static __device__ __forceinline__ int index(T k) { return (int)(0xFFFFu - (k & 0xFFFFu)); }
+  static __device__ __forceinline__ float value(T k) {
+    const uint32_t b = k >> 16;
+    return __uint_as_float(((b & 0x8000u) ? (b & 0x7FFFu) : (~b & 0xFFFFu)) << 16);
+  }
+  static __device__ __forceinline__ T row_max(T k) {
+    return row_max_keys<T, dpp_u32<0xB1>, dpp_u32<0x4E>, dpp_u32<0x141>, dpp_u32<0x140>>(k);
+  }
+  static __device__ __forceinline__ T readlane(T k, int lane) {
+    return (T)__builtin_amdgcn_readlane((int)k, lane);
+  }
+};
+
 __device__ __forceinline__ float row_sum_f32(float v) {
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
   return v;
-}
-__device__ __forceinline__ unsigned long long readlane_u64(unsigned long long k, int lane) {
-  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)k, lane);
-  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), lane);
-  return ((unsigned long long)hi << 32) | lo;
 }
 
 // LDS scratch of one top-k wave, in 64-bit words: 4 rows x 16 candidates
@@ -234,20 +265,18 @@ constexpr int kTopkScratch = 80;
 // round trips), then every one of the 4 K row winners takes its rank among
 // all of them from LDS; the K best ranks are the selection.  K <= 16,
 // E <= 256.  The probability sum runs in selection order.
-// topk_wave_v takes lane l's logits of experts 4 l .. 4 l + 3 already loaded
-// (-INFINITY past E); topk_wave loads them from lg.
-__device__ __forceinline__ void topk_wave_v(const float vin[4], int E, int K, int lane,
-                                            unsigned long long *scratch, int64_t *ids_out,
-                                            uint16_t *w_out) {
-  unsigned long long key[4];
-  float v[4];
+template <class KT>
+__device__ __forceinline__ void topk_wave_keys(const float v[4], int E, int K, int lane,
+                                               unsigned long long *scratch_words, int64_t *ids_out,
+                                               uint16_t *w_out) {
+  using T = typename KT::T;
+  T *scratch = reinterpret_cast<T *>(scratch_words);
+  T key[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = vin[j];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) key[j] = lane * 4 + j < E ? topk_key(v[j], lane * 4 + j) : 0ull;
+  for (int j = 0; j < 4; ++j) key[j] = lane * 4 + j < E ? KT::make(v[j], lane * 4 + j) : (T)0;
   auto cswap = [&](int a, int b) {
     if (key[a] < key[b]) {
-      const unsigned long long tmp = key[a];
+      const T tmp = key[a];
       key[a] = key[b];
       key[b] = tmp;
     }
@@ -258,18 +287,18 @@ __device__ __forceinline__ void topk_wave_v(const float vin[4], int E, int K, in
   cswap(1, 3);
   cswap(1, 2);
   // Row-local top K: the lane holding a row's maximum pops it.
-  unsigned long long top[16];
+  T top[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    top[i] = 0ull;
+    top[i] = 0;
     if (i < K) {
-      const unsigned long long m = row_max_u64(key[0]);
+      const T m = KT::row_max(key[0]);
       top[i] = m;
       if (key[0] == m) {
         key[0] = key[1];
         key[1] = key[2];
         key[2] = key[3];
-        key[3] = 0ull;
+        key[3] = 0;
       }
     }
   }
@@ -278,13 +307,13 @@ __device__ __forceinline__ void topk_wave_v(const float vin[4], int E, int K, in
   for (int i = 0; i < 16; ++i)
     if (i < K && (lane & 15) == i) scratch[row * K + i] = top[i];
   // Softmax statistics: the global maximum is the best of the row maxima.
-  unsigned long long mk = readlane_u64(top[0], 0);
+  T mk = KT::readlane(top[0], 0);
 #pragma unroll
   for (int r = 1; r < 4; ++r) {
-    const unsigned long long o = readlane_u64(top[0], 16 * r);
+    const T o = KT::readlane(top[0], 16 * r);
     mk = o > mk ? o : mk;
   }
-  const float mx = topk_key_value(mk);
+  const float mx = KT::value(mk);
   float part = 0.0f;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -298,13 +327,13 @@ __device__ __forceinline__ void topk_wave_v(const float vin[4], int E, int K, in
   // Rank of each row winner among all 4 K of them (keys are distinct; the
   // 0 keys of missing experts rank last).
   const int nc = 4 * K;
-  const unsigned long long mine = lane < nc ? scratch[lane] : 0ull;
+  const T mine = lane < nc ? scratch[lane] : (T)0;
   int rank = 0;
 #pragma unroll 8
   for (int j = 0; j < nc; ++j) rank += scratch[j] > mine ? 1 : 0;
-  float *prob = reinterpret_cast<float *>(scratch + 64);
+  float *prob = reinterpret_cast<float *>(scratch_words + 64);
   const bool chosen = lane < nc && rank < K;
-  const float pe = expf(topk_key_value(mine) - mx) / denom;
+  const float pe = expf(KT::value(mine) - mx) / denom;
   if (chosen) prob[rank] = pe;
   __builtin_amdgcn_wave_barrier();
   float psum = 0.0f;
@@ -312,9 +341,24 @@ __device__ __forceinline__ void topk_wave_v(const float vin[4], int E, int K, in
   for (int i = 0; i < 16; ++i)
     if (i < K) psum += prob[i];
   if (chosen) {
-    ids_out[rank] = topk_key_index(mine);
+    ids_out[rank] = KT::index(mine);
     w_out[rank] = f32_to_bf16_bits(pe / psum);
   }
+}
+
+// topk_wave_v takes lane l's logits of experts 4 l .. 4 l + 3 already loaded
+// (-INFINITY past E); topk_wave loads them from lg.  The whole wave must be
+// active.  When every logit of the token is a bf16 value the selection runs
+// on 32-bit keys; both key widths order the keys identically.
+__device__ __forceinline__ void topk_wave_v(const float v[4], int E, int K, int lane,
+                                            unsigned long long *scratch, int64_t *ids_out,
+                                            uint16_t *w_out) {
+  const uint32_t low = (__float_as_uint(v[0]) | __float_as_uint(v[1]) | __float_as_uint(v[2]) |
+                        __float_as_uint(v[3])) & 0xFFFFu;
+  if (__all(low == 0u))
+    topk_wave_keys<Key32>(v, E, K, lane, scratch, ids_out, w_out);
+  else
+    topk_wave_keys<Key64>(v, E, K, lane, scratch, ids_out, w_out);
 }
 
 __device__ __forceinline__ void topk_wave(const float *lg, int E, int K, int lane,

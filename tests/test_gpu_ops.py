@@ -247,6 +247,30 @@ def test_router_ties_lowest_id(dev):
     assert np.all(npf(wz) == O.bf16(np.float32(0.125)))
 
 
+@pytest.mark.parametrize('bias_kind', ['none', 'zero', 'tiny'])
+def test_router_key_widths(dev, bias_kind):
+    # Logits that are all bf16 values select on 32-bit keys, any other fp32
+    # logits on 64-bit keys.  A zero bias keeps every logit a bf16 value; a
+    # bias of 2^-20 multiples does not.  All logits are <= 0 (signed-key
+    # order, -0 against +0) and rows of w repeat (exact ties).
+    gen = seeded(12)
+    x = bf16_rand((37, 2048), gen).abs()
+    w = -bf16_rand((256, 2048), gen, 0.02).abs()
+    w[9] = w[130]
+    w[240] = w[130]
+    w[17:40] = 0
+    x[5] = 0
+    bias = {'none': None, 'zero': np.zeros(256, np.float32),
+            'tiny': (np.arange(256) % 7).astype(np.float32) * np.float32(2.0 ** -20)}[bias_kind]
+    lg, wts, ids = router.router_topk(x.to(dev), w.to(dev), 8,
+                                      None if bias is None else torch.from_numpy(bias))
+    rl, rw, ri = O.router(npf(x), npf(w), 8, bias)
+    assert np.array_equal(lg.cpu().numpy(), rl)
+    assert np.array_equal(ids.cpu().numpy(), ri)
+    assert np.abs(npf(wts) - rw).max() <= 2.0 ** -8
+    assert ids[5].cpu().tolist() == ri[5].tolist()
+
+
 def test_rmsnorm_bit_exact(dev):
     gen = seeded(11)
     x = bf16_rand((5, 2048), gen, 3.0)
