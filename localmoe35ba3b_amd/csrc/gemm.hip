@@ -449,7 +449,10 @@ __device__ __forceinline__ void barrier_raw() { asm volatile("s_barrier" ::: "me
 // MFMA as the B operand.  Only the activation rows (shared by the four
 // waves) are staged in LDS, in a 3-slot ring loaded through registers one
 // stage ahead of their LDS write.  All loads are ordinary compiler-tracked
-// loads, so every wait the compiler inserts is exact.
+// loads, so every wait the compiler inserts is exact.  Within a stage the
+// dequantization of the next 8-K piece is interleaved with the MFMAs of the
+// current one (one MFMA, then a few VALU ops), so a wave keeps the matrix
+// pipe and the VALU busy together.
 //
 // K order inside a 64-K stage: lane l (quad q = l >> 4) loads 16 consecutive
 // weights k = 16 q .. 16 q + 15 of its column; MFMA step `sub` takes the
@@ -579,10 +582,17 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Prologue: A(0) into LDS; A(1 .. AD-1) and B(0 .. BD-2) in flight.
-  load_a(0, 0);
+  // Prologue: A(0) into LDS; A(1 .. AD-1) and B(0 .. BD-2) in flight.  All
+  // of them are requested before the first wait, so the tile pays one load
+  // latency before its first stage (A(0) goes through registers of its own).
+  u32x4 a0[A_W];
+#pragma unroll
+  for (int j = 0; j < A_W; ++j) a0[j] = ldg16(asrc[j]);
 #pragma unroll
   for (int s = 0; s < BD - 1; ++s) load_b(s, s);
+#pragma unroll
+  for (int s = 1; s < AD; ++s)
+    if (s < KT) load_a(s % AS, s);
 #pragma unroll
   for (int j = 0; j < SC_W; ++j) {
     const int piece = tid + NT * j;
@@ -592,48 +602,69 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
       for (int i = 0; i < 4; ++i) scl[(g0 + i) * BN + c] = __uint_as_float(sreg[j][i]);
     }
   }
-  store_a(0, 0);
 #pragma unroll
-  for (int s = 1; s < AD; ++s)
-    if (s < KT) load_a(s % AS, s);
+  for (int j = 0; j < A_W; ++j)
+    *reinterpret_cast<u32x4 *>(smem + (NW * j + wave) * 1024 + lane * 16) = a0[j];
 
-  // Stage s: publish A(s+1), barrier, request A(s+AD) and B(s+BD-1) (into the
-  // slots freed by the previous stage), then dequantize B(s) and run the MFMAs.
-  auto step = [&](int s, int ub, int ua, bool st_a, bool ld_a, bool ld_b) {
+  // Piece p of a stage (h = p / 2, sub = p % 2): 8 K per lane per column
+  // sub-tile.  dq dequantizes one piece of stage s from weight slot ub.
+  constexpr int P = 2 * HL;
+  auto dq = [&](int ub, int s, int p, u32x4 *out) {
+    const int g = (s * KS) >> 7;
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) {
+      const float sc = scl[g * BN + col_base(ni) + (lane & 15)];
+      out[ni] = dequant8s_bf16(
+          uint2{breg[ub][ni][p >> 1][2 * (p & 1)], breg[ub][ni][p >> 1][2 * (p & 1) + 1]}, sc);
+    }
+  };
+  // The B operand of the piece being multiplied; the next piece (the first
+  // piece of the next stage, after a stage's last) is dequantized while the
+  // MFMAs of this one run.
+  u32x4 bcur[NI];
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  barrier_raw();
+  dq(0, 0, 0, bcur);
+  constexpr int VG = (20 * NI + MS * NI - 1) / (MS * NI);  // dequant VALU per MFMA
+  auto step = [&](int s, int ub, int ua, bool st_a, bool ld_a, bool ld_b, bool has_next) {
     if (st_a) store_a(ua, s + 1);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
     barrier_raw();
     if (ld_a) load_a(ua, s + AD);
     if (ld_b) load_b((ub + BD - 1) % BD, s + BD - 1);
-    // keep the requests at the top of the stage: left to itself the scheduler
-    // sinks them below the MFMAs, which shortens the prefetch by a stage
     __builtin_amdgcn_sched_barrier(0);
     const unsigned char *sa = smem + (s % AR) * A_STAGE;
-    const int g = (s * KS) >> 7;
-    float sc[NI];
 #pragma unroll
-    for (int ni = 0; ni < NI; ++ni) sc[ni] = scl[g * BN + col_base(ni) + (lane & 15)];
+    for (int p = 0; p < P; ++p) {
+      u32x4 af[MS];
 #pragma unroll
-    for (int h = 0; h < HL; ++h) {
+      for (int mi = 0; mi < MS; ++mi) {
+        const int r = mi * 16 + (lane & 15);
+        af[mi] = *reinterpret_cast<const u32x4 *>(
+            sa + r * ROWB + (((8 * (p >> 1) + 2 * q + (p & 1)) ^ rb_swz(r)) * 16));
+      }
+      const bool nxt = p + 1 < P || has_next;
+      u32x4 bn[NI];
+      if (p + 1 < P)
+        dq(ub, s, p + 1, bn);
+      else if (has_next)
+        dq((ub + 1) % BD, s + 1, 0, bn);
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        u32x4 af[MS];
-#pragma unroll
-        for (int mi = 0; mi < MS; ++mi) {
-          const int r = mi * 16 + (lane & 15);
-          af[mi] = *reinterpret_cast<const u32x4 *>(
-              sa + r * ROWB + (((8 * h + 2 * q + sub) ^ rb_swz(r)) * 16));
-        }
-        u32x4 bfr[NI];
+      for (int mi = 0; mi < MS; ++mi)
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni)
-          bfr[ni] = dequant8s_bf16(uint2{breg[ub][ni][h][2 * sub], breg[ub][ni][h][2 * sub + 1]},
-                                   sc[ni]);
+          acc[mi][ni] = BF16::mfma16x16x32(af[mi], bcur[ni], acc[mi][ni]);
+      __builtin_amdgcn_sched_group_barrier(0x100, MS, 0);
+      if (nxt) __builtin_amdgcn_sched_group_barrier(0x002, 2 * VG, 0);
 #pragma unroll
-        for (int mi = 0; mi < MS; ++mi)
+      for (int i = 0; i < MS * NI; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (nxt) __builtin_amdgcn_sched_group_barrier(0x002, VG, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (nxt) {
 #pragma unroll
-          for (int ni = 0; ni < NI; ++ni)
-            acc[mi][ni] = BF16::mfma16x16x32(af[mi], bfr[ni], acc[mi][ni]);
+        for (int ni = 0; ni < NI; ++ni) bcur[ni] = bn[ni];
       }
     }
   };
@@ -645,12 +676,12 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   static_assert(TL <= KT, "stage count");
   for (int s0 = 0; s0 < KT - TL; s0 += U) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) step(s0 + u, u % BD, (u + 1) % AS, true, true, true);
+    for (int u = 0; u < U; ++u) step(s0 + u, u % BD, (u + 1) % AS, true, true, true, true);
   }
 #pragma unroll
   for (int v = 0; v < TL; ++v) {
     const int s = KT - TL + v;
-    step(s, s % BD, (s + 1) % AS, s + 1 < KT, s + AD < KT, s + BD - 1 < KT);
+    step(s, s % BD, (s + 1) % AS, s + 1 < KT, s + AD < KT, s + BD - 1 < KT, s + 1 < KT);
   }
 
 #pragma unroll
@@ -725,6 +756,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
 #ifndef LM_RB_NW
 #define LM_RB_NW 4
 #endif
+
 
 #ifndef LM_GROUPED_BN
 #define LM_GROUPED_BN 128
