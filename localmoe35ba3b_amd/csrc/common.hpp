@@ -136,6 +136,29 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+// Full 64-lane fp64 sum without LDS round trips: DPP sums inside each
+// 16-lane row, then the four row sums through readlane.  The summands here
+// are exact products whose sum fp64 holds exactly, so the order is free.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const unsigned long long b = __double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  const unsigned long long b = __double_as_longlong(v);
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)b, lane);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ double wave_sum_f64_dpp(double v) {
+  v += dpp_f64<0xB1>(v);
+  v += dpp_f64<0x4E>(v);
+  v += dpp_f64<0x141>(v);
+  v += dpp_f64<0x140>(v);
+  return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
+}
 __device__ __forceinline__ float wave_max_f32(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -265,15 +288,13 @@ constexpr int kTopkScratch = 80;
 // round trips), then every one of the 4 K row winners takes its rank among
 // all of them from LDS; the K best ranks are the selection.  K <= 16,
 // E <= 256.  The probability sum runs in selection order.
+// Sorts a lane's 4 keys, then finds each 16-lane row's top K by DPP maxima
+// (the lane holding a row's maximum pops it) and writes the 4 K row winners
+// to scratch[row * K + i].  Returns the lane's row maximum.
 template <class KT>
-__device__ __forceinline__ void topk_wave_keys(const float v[4], int E, int K, int lane,
-                                               unsigned long long *scratch_words, int64_t *ids_out,
-                                               uint16_t *w_out) {
+__device__ __forceinline__ typename KT::T topk_row_winners(typename KT::T key[4], int K, int lane,
+                                                          typename KT::T *scratch) {
   using T = typename KT::T;
-  T *scratch = reinterpret_cast<T *>(scratch_words);
-  T key[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) key[j] = lane * 4 + j < E ? KT::make(v[j], lane * 4 + j) : (T)0;
   auto cswap = [&](int a, int b) {
     if (key[a] < key[b]) {
       const T tmp = key[a];
@@ -286,7 +307,6 @@ __device__ __forceinline__ void topk_wave_keys(const float v[4], int E, int K, i
   cswap(0, 2);
   cswap(1, 3);
   cswap(1, 2);
-  // Row-local top K: the lane holding a row's maximum pops it.
   T top[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -306,6 +326,51 @@ __device__ __forceinline__ void topk_wave_keys(const float v[4], int E, int K, i
 #pragma unroll
   for (int i = 0; i < 16; ++i)
     if (i < K && (lane & 15) == i) scratch[row * K + i] = top[i];
+  return top[0];
+}
+
+// Rank of row winner `lane` among all 4 K of them (keys are distinct; 0
+// keys rank last); lanes >= 4 K get 0 keys.
+template <class KT>
+__device__ __forceinline__ int topk_winner_rank(const typename KT::T *scratch, int K, int lane,
+                                                typename KT::T &mine) {
+  using T = typename KT::T;
+  const int nc = 4 * K;
+  mine = lane < nc ? scratch[lane] : (T)0;
+  int rank = 0;
+#pragma unroll 8
+  for (int j = 0; j < nc; ++j) rank += scratch[j] > mine ? 1 : 0;
+  return rank;
+}
+
+// The K-th largest of the wave's 256 keys (4 per lane), in every lane.
+template <class KT>
+__device__ __forceinline__ typename KT::T kth_key_wave(typename KT::T key[4], int K, int lane,
+                                                      unsigned long long *scratch_words) {
+  using T = typename KT::T;
+  T *scratch = reinterpret_cast<T *>(scratch_words);
+  topk_row_winners<KT>(key, K, lane, scratch);
+  __builtin_amdgcn_wave_barrier();
+  T mine;
+  const int rank = topk_winner_rank<KT>(scratch, K, lane, mine);
+  __builtin_amdgcn_wave_barrier();
+  T *out = reinterpret_cast<T *>(scratch_words + 64);
+  if (lane < 4 * K && rank == K - 1) out[0] = mine;
+  __builtin_amdgcn_wave_barrier();
+  return out[0];
+}
+
+template <class KT>
+__device__ __forceinline__ void topk_wave_keys(const float v[4], int E, int K, int lane,
+                                               unsigned long long *scratch_words, int64_t *ids_out,
+                                               uint16_t *w_out) {
+  using T = typename KT::T;
+  T *scratch = reinterpret_cast<T *>(scratch_words);
+  T key[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) key[j] = lane * 4 + j < E ? KT::make(v[j], lane * 4 + j) : (T)0;
+  const T rowmax = topk_row_winners<KT>(key, K, lane, scratch);
+  T top[1] = {rowmax};
   // Softmax statistics: the global maximum is the best of the row maxima.
   T mk = KT::readlane(top[0], 0);
 #pragma unroll
@@ -324,13 +389,10 @@ __device__ __forceinline__ void topk_wave_keys(const float v[4], int E, int K, i
                       (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 32)) +
                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 48)));
   __builtin_amdgcn_wave_barrier();
-  // Rank of each row winner among all 4 K of them (keys are distinct; the
-  // 0 keys of missing experts rank last).
+  // Rank of each row winner among all 4 K of them.
   const int nc = 4 * K;
-  const T mine = lane < nc ? scratch[lane] : (T)0;
-  int rank = 0;
-#pragma unroll 8
-  for (int j = 0; j < nc; ++j) rank += scratch[j] > mine ? 1 : 0;
+  T mine;
+  const int rank = topk_winner_rank<KT>(scratch, K, lane, mine);
   float *prob = reinterpret_cast<float *>(scratch_words + 64);
   const bool chosen = lane < nc && rank < K;
   const float pe = expf(KT::value(mine) - mx) / denom;

@@ -28,11 +28,12 @@ constexpr int kI = 512;
 constexpr int kE = 256;
 constexpr int kTopK = 8;
 constexpr int kBM = 96;  // prefill MFMA tile height (one tile covers a typical expert)
+constexpr int kTopkTokens = 8;  // prefill top-k: tokens (waves) per workgroup
 static_assert(kE == 256, "the prefill kernels map one thread of a 256-thread workgroup to each expert");
 
 struct WsLayout {
-  int64_t ctr, bcounts, xn, gl, logits, ids, wts, sel, selw, xq, xs, pos, table, rslot, rpos, hbuf,
-      vbuf, total;
+  int64_t ctr, bcounts, xn, gl, logits, nx, nw, ids, wts, sel, selw, xq, xs, pos, table, rslot,
+      rpos, hbuf, vbuf, total;
   int64_t max_tiles, n_tiles;
 };
 
@@ -53,6 +54,8 @@ static WsLayout layout(int64_t T) {
   w.xn = take(T * kH * 2);
   w.gl = take(T * 4);
   w.logits = take(T * kE * 4);
+  w.nx = take(T * 4);
+  w.nw = take(kE * 4);
   w.ids = take(T * kTopK * 8);
   w.wts = take(T * kTopK * 2);
   w.sel = take(kTopK * 4);
@@ -61,7 +64,7 @@ static WsLayout layout(int64_t T) {
   w.xs = take(kH / 128 * 4);
   w.pos = take((R + T) * 8);
   w.table = take(w.n_tiles * 3 * 8);
-  w.bcounts = take((T + 15) / 16 * kE * 4);  // per top-k workgroup expert counts
+  w.bcounts = take((T + kTopkTokens - 1) / kTopkTokens * kE * 4);  // per top-k workgroup expert counts
   w.rslot = take(R * 4);  // rank of each route inside its top-k workgroup and expert
   w.rpos = take(R * 4);   // sorted row of each route
   w.hbuf = take((R + T) * kI * 2);
@@ -87,6 +90,8 @@ struct LayerArgs {
   uint16_t *xn;
   float *gl;
   float *logits;
+  float *nx;  // prefill: |xn| of each token row
+  float *nw;  // prefill: |w_e| of each router row
   int64_t *ids;
   uint16_t *wts;
   int *sel;
@@ -453,15 +458,40 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
 }
 
 // ------------------------------------------------------------------ prefill
-// RMSNorm of each token row + the shared-expert gate logit (fp64 dot).
-__global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a) {
+// RMSNorm of each token row + the shared-expert gate logit (fp64 dot) + the
+// Euclidean norms that bound the approximate router logits: |xn| of each
+// token (workgroups < T) and |w_e| of each router row (workgroups < kE).
+__global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a, int T) {
   __shared__ float xf[kH];
   __shared__ float red[4];
+  __shared__ float red2[4];
   __shared__ double dred[4];
   const int tok = blockIdx.x;
   const int t = threadIdx.x;
-  norm_row_to_lds(a.h + (int64_t)tok * kH, a.norm_w, a.eps, xf, red);
   constexpr int PER = kH / 256;
+  if (tok < kE) {
+    const u32x4 wv = ldg16(a.router_w + (int64_t)tok * kH + t * PER);
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = bf16_bits_to_f32(wv[j] & 0xFFFFu), hi = bf16_bits_to_f32(wv[j] >> 16);
+      ss += lo * lo + hi * hi;
+    }
+    ss = wave_sum_f32(ss);
+    if ((t & 63) == 0) red2[t >> 6] = ss;
+    __syncthreads();
+    if (t == 0) a.nw[tok] = sqrtf((red2[0] + red2[1]) + (red2[2] + red2[3]));
+    __syncthreads();
+  }
+  if (tok >= T) return;
+  norm_row_to_lds(a.h + (int64_t)tok * kH, a.norm_w, a.eps, xf, red);
+  {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) ss += xf[t * PER + j] * xf[t * PER + j];
+    ss = wave_sum_f32(ss);
+    if ((t & 63) == 0) red2[t >> 6] = ss;
+  }
   u32x4 packed;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -477,7 +507,244 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a) {
   acc = wave_sum_f64(acc);
   if ((t & 63) == 0) dred[t >> 6] = acc;
   __syncthreads();
-  if (t == 0) a.gl[tok] = round_bf16((float)(dred[0] + dred[1] + dred[2] + dred[3]));
+  if (t == 0) {
+    a.gl[tok] = round_bf16((float)(dred[0] + dred[1] + dred[2] + dred[3]));
+    a.nx[tok] = sqrtf((red2[0] + red2[1]) + (red2[2] + red2[3]));
+  }
+}
+
+// Approximate router logits of the prefill tokens: bf16 MFMA with fp32
+// accumulation (neither rounded to bf16 nor biased).  A workgroup owns 32
+// tokens x 64 experts; its four waves each take one quarter of K for the
+// whole tile (2 x 4 MFMA tiles, so every 16-byte row piece loaded feeds two
+// or four MFMAs) and the quarters are summed through LDS at the end.  K is
+// streamed in 32-wide stages through a kRaD-deep register ring.  The
+// summation order does not matter: prefill_topk_count_kernel bounds the
+// error of any order.
+constexpr int kRaTok = 32, kRaExp = 64, kRaD = 4;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void
+router_approx_kernel(LayerArgs a, int T) {
+  constexpr int KQ = kH / 4;
+  constexpr int NS = KQ / 32;
+  static_assert(NS % kRaD == 0 && kE % kRaExp == 0, "router tiling");
+  __shared__ f32x4 part[3][8][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int t0 = blockIdx.x * kRaTok;
+  const int e0 = blockIdx.y * kRaExp;
+  const int kb = wave * KQ + q * 8;
+  const uint16_t *xa[2], *wb[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) xa[i] = a.xn + (int64_t)min(t0 + 16 * i + r, T - 1) * kH + kb;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) wb[j] = a.router_w + (int64_t)(e0 + 16 * j + r) * kH + kb;
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 ra[kRaD][2], rb[kRaD][4];
+  auto load = [&](int slot, int st) {
+    const int k = min(st, NS - 1) * 32;  // past the end the last stage is re-read, never used
+#pragma unroll
+    for (int i = 0; i < 2; ++i) ra[slot][i] = ldg16(xa[i] + k);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) rb[slot][j] = ldg16(wb[j] + k);
+  };
+#pragma unroll
+  for (int d = 0; d < kRaD; ++d) load(d, d);
+  for (int s0 = 0; s0 < NS; s0 += kRaD) {
+#pragma unroll
+    for (int u = 0; u < kRaD; ++u) {
+      u32x4 av[2], bv[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) av[i] = ra[u][i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = rb[u][j];
+      load(u, s0 + u + kRaD);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = BF16::mfma16x16x32(av[i], bv[j], acc[i][j]);
+      // one stage per scheduling region: the refills stay kRaD stages ahead
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) part[wave - 1][4 * i + j][lane] = acc[i][j];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 v = acc[i][j] + part[0][4 * i + j][lane] + part[1][4 * i + j][lane] +
+                      part[2][4 * i + j][lane];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int t = t0 + 16 * i + 4 * q + m;
+        if (t < T) a.logits[(int64_t)t * kE + e0 + 16 * j + r] = v[m];
+      }
+    }
+}
+
+// Exact top-8 of one prefill token (one wave) from the approximate logits.
+// An approximate logit A is the fp32 sum of the exactly representable
+// bf16 x bf16 products with at most kH + kH / 32 fp32 roundings, so
+// |A - S| <= (kH + kH / 32) 2^-23 sum_k |x_k w_ek| <= 2^-11 |x| |w_e| / 1.01
+// for the exact dot product S (Cauchy-Schwarz; the 1% absorbs the
+// rounding of the norms and of A -/+ eps).  Rounding to bf16 and adding the
+// bias are monotone, so the exact logit round_bf16(S) (+ bias) lies in
+// [round_bf16(A - eps), round_bf16(A + eps)] (+ bias).  With T8 the 8th largest
+// lower-bound key, an expert whose upper-bound key is below T8 is beaten by
+// 8 experts whatever its exact logit is; every other expert (a candidate,
+// typically 8 to 10) gets its exact logit from an fp64 dot product, the same
+// value router_logits computes.  The selection and softmax then run on
+// exact logits for the candidates and rounded approximate ones elsewhere,
+// which can only enter the softmax denominator.
+template <class KT>
+__device__ void topk_exact_wave(const LayerArgs &a, int tok, int lane, unsigned long long *scratch,
+                                float *lv, int *cand, int64_t *ids_out, uint16_t *w_out) {
+  using T = typename KT::T;
+  u32x4 xv[4];  // the token's row, needed once the candidates are known
+  {
+    const uint16_t *xr = a.xn + (int64_t)tok * kH + lane * 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xv[i] = ldg16(xr + 512 * i);
+  }
+  const float4 av = *reinterpret_cast<const float4 *>(a.logits + (int64_t)tok * kE + lane * 4);
+  const float4 nv = *reinterpret_cast<const float4 *>(a.nw + lane * 4);
+  const float nx = a.nx[tok];
+  const float A[4] = {av.x, av.y, av.z, av.w};
+  const float NW[4] = {nv.x, nv.y, nv.z, nv.w};
+  float lo[4], hi[4];
+  T klo[4], khi[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane * 4 + j;
+    const float eps = 0x1.0p-11f * 1.01f * (nx * NW[j]) + 1e-30f;
+    lo[j] = round_bf16(A[j] - eps);
+    hi[j] = round_bf16(A[j] + eps);
+    float ap = round_bf16(A[j]);
+    if (a.router_bias) {
+      const float b = a.router_bias[e];
+      lo[j] = lo[j] + b;
+      hi[j] = hi[j] + b;
+      ap = ap + b;
+    }
+    lv[e] = ap;
+    klo[j] = KT::make(lo[j], e);
+    khi[j] = KT::make(hi[j], e);
+  }
+  const T t8 = kth_key_wave<KT>(klo, kTopK, lane, scratch);
+  // candidates, compacted into cand[0 .. n)
+  int n = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bool c = khi[j] >= t8;
+    const unsigned long long m = __ballot(c);
+    const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
+    const int before = (int)__builtin_amdgcn_mbcnt_hi(mhi, __builtin_amdgcn_mbcnt_lo(mlo, 0u));
+    if (c) cand[n + before] = lane * 4 + j;
+    n += __popcll(m);
+  }
+  __builtin_amdgcn_wave_barrier();
+  // exact logits, CB candidates per batch, the next batch's rows requested
+  // before the current batch is reduced: lane holds x[k] and w[k] for
+  // k = 8 lane + 512 i + (0..7)
+  constexpr int CB = 3;
+  u32x4 wv[2][CB][4];
+  int ec[2][CB];
+  auto fetch = [&](int buf, int c0) {
+#pragma unroll
+    for (int b = 0; b < CB; ++b) {
+      ec[buf][b] = cand[min(c0 + b, n - 1)];
+      const uint16_t *wr = a.router_w + (int64_t)ec[buf][b] * kH + lane * 8;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wv[buf][b][i] = ldg16(wr + 512 * i);
+    }
+  };
+  auto reduce = [&](int buf, int c0) {
+    double acc[CB];
+#pragma unroll
+    for (int b = 0; b < CB; ++b) {
+      acc[b] = 0.0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[b] = __builtin_fma((double)bf16_bits_to_f32(xv[i][j] & 0xFFFFu),
+                                 (double)bf16_bits_to_f32(wv[buf][b][i][j] & 0xFFFFu), acc[b]);
+          acc[b] = __builtin_fma((double)bf16_bits_to_f32(xv[i][j] >> 16),
+                                 (double)bf16_bits_to_f32(wv[buf][b][i][j] >> 16), acc[b]);
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < CB; ++b) {
+      const double sum = wave_sum_f64_dpp(acc[b]);
+      if (lane == 0 && c0 + b < n) {
+        float l = round_bf16((float)sum);
+        if (a.router_bias) l = l + a.router_bias[ec[buf][b]];
+        lv[ec[buf][b]] = l;
+      }
+    }
+  };
+  fetch(0, 0);
+  for (int c0 = 0; c0 < n; c0 += 2 * CB) {
+    if (c0 + CB < n) fetch(1, c0 + CB);
+    reduce(0, c0);
+    if (c0 + 2 * CB < n) fetch(0, c0 + 2 * CB);
+    if (c0 + CB < n) reduce(1, c0 + CB);
+  }
+  __builtin_amdgcn_wave_barrier();
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = lv[lane * 4 + j];
+  if (n > 64) {  // more candidates than lanes: the full top-k over lv
+    topk_wave_v(v, kE, kTopK, lane, scratch, ids_out, w_out);
+    return;
+  }
+  // Selection among the candidates (lane c holds candidate c); every
+  // non-candidate ranks below 8 candidates.  The softmax follows
+  // topk_wave_keys operation for operation, so the result is the one the
+  // full top-k over lv gives.
+  T *keys = reinterpret_cast<T *>(scratch);
+  const bool has = lane < n;
+  const int ce = has ? cand[lane] : 0;
+  const float cv = has ? lv[ce] : 0.0f;
+  const T ck = has ? KT::make(cv, ce) : (T)0;
+  keys[lane] = ck;
+  __builtin_amdgcn_wave_barrier();
+  int rank = 0;
+  for (int c = 0; c < n; ++c) rank += keys[c] > ck ? 1 : 0;
+  const unsigned long long first = __ballot(has && rank == 0);
+  const float mx = __int_as_float(__builtin_amdgcn_readlane(
+      __float_as_int(KT::value(ck)), (int)__builtin_ctzll(first)));
+  float part = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) part += expf(v[j] - mx);
+  part = row_sum_f32(part);
+  const float denom = (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 0)) +
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16))) +
+                      (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 32)) +
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 48)));
+  float *prob = reinterpret_cast<float *>(scratch + 64);
+  const bool chosen = has && rank < kTopK;
+  const float pe = expf(KT::value(ck) - mx) / denom;
+  if (chosen) prob[rank] = pe;
+  __builtin_amdgcn_wave_barrier();
+  float psum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kTopK; ++i) psum += prob[i];
+  if (chosen) {
+    ids_out[rank] = ce;
+    w_out[rank] = f32_to_bf16_bits(pe / psum);
+  }
 }
 
 // Top-k of every prefill token (one wave per token, kTopkTokens tokens per
@@ -488,18 +755,20 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a) {
 // bcounts.  Rows of one expert are in no particular order - the grouped
 // GEMMs compute every row independently and the combine walks a token's
 // routes in ascending expert id, so the layer output does not depend on it.
-constexpr int kTopkTokens = 16;
 constexpr int kScanRoutes = 1024;  // routes per prefill_scan_kernel workgroup
 constexpr int kScanGroups = kScanRoutes / (kTopkTokens * kTopK);  // top-k workgroups per scan one
 static_assert(kScanGroups * kTopkTokens * kTopK == kScanRoutes, "scan slices whole top-k groups");
 
-__global__ __launch_bounds__(1024) void prefill_topk_count_kernel(LayerArgs a, int T, int *bcounts,
-                                                                  int *rslot) {
+__global__ __launch_bounds__(kTopkTokens * 64) void prefill_topk_count_kernel(LayerArgs a, int T,
+                                                                             int *bcounts,
+                                                                             int *rslot) {
   __shared__ int lcnt[kE];
-  __shared__ int64_t sid[16][kTopK];
-  __shared__ uint16_t swt[16][kTopK];
-  __shared__ unsigned long long scratch[16][kTopkScratch];
-  static_assert(kTopkTokens == 16, "one wave per token");
+  __shared__ int64_t sid[kTopkTokens][kTopK];
+  __shared__ uint16_t swt[kTopkTokens][kTopK];
+  __shared__ unsigned long long scratch[kTopkTokens][kTopkScratch];
+  __shared__ float lv[kTopkTokens][kE];
+  __shared__ int cand[kTopkTokens][kE];
+  static_assert(kTopkTokens * 64 >= kE, "one thread per expert count");
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int w = t >> 6;
@@ -508,7 +777,10 @@ __global__ __launch_bounds__(1024) void prefill_topk_count_kernel(LayerArgs a, i
   const int tok = blockIdx.x * kTopkTokens + w;
   int e = -1, rank = 0;
   if (tok < T) {  // wave-uniform
-    topk_wave(a.logits + (int64_t)tok * kE, kE, kTopK, lane, scratch[w], sid[w], swt[w]);
+    if (a.router_bias)
+      topk_exact_wave<Key64>(a, tok, lane, scratch[w], lv[w], cand[w], sid[w], swt[w]);
+    else
+      topk_exact_wave<Key32>(a, tok, lane, scratch[w], lv[w], cand[w], sid[w], swt[w]);
     __builtin_amdgcn_wave_barrier();
     if (lane < kTopK) {
       e = (int)sid[w][lane];
@@ -747,6 +1019,8 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   a.xn = reinterpret_cast<uint16_t *>(ws + w.xn);
   a.gl = reinterpret_cast<float *>(ws + w.gl);
   a.logits = reinterpret_cast<float *>(ws + w.logits);
+  a.nx = reinterpret_cast<float *>(ws + w.nx);
+  a.nw = reinterpret_cast<float *>(ws + w.nw);
   a.ids = reinterpret_cast<int64_t *>(ws + w.ids);
   a.wts = reinterpret_cast<uint16_t *>(ws + w.wts);
   a.sel = reinterpret_cast<int *>(ws + w.sel);
@@ -786,13 +1060,14 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   int *rpos = reinterpret_cast<int *>(ws + w.rpos);
   uint16_t *vbuf = reinterpret_cast<uint16_t *>(ws + w.vbuf);
   if (int rc = mark(0)) return rc;
-  prefill_norm_gate_kernel<<<(unsigned)T, 256, 0, st>>>(a);
+  prefill_norm_gate_kernel<<<(unsigned)(T > kE ? T : kE), 256, 0, st>>>(a, (int)T);
   if (int rc = check_launch("prefill_norm_gate_kernel")) return rc;
   if (int rc = mark(1)) return rc;
-  if (int rc = router_logits(a.xn, a.router_w, a.router_bias, a.logits, T, kE, kH, st)) return rc;
+  router_approx_kernel<<<dim3(cdiv(T, kRaTok), kE / kRaExp), 256, 0, st>>>(a, (int)T);
+  if (int rc = check_launch("router_approx_kernel")) return rc;
   if (int rc = mark(2)) return rc;
   const int nb = (int)cdiv(T, kTopkTokens);
-  prefill_topk_count_kernel<<<nb, 1024, 0, st>>>(a, (int)T, bcounts, rslot);
+  prefill_topk_count_kernel<<<nb, kTopkTokens * 64, 0, st>>>(a, (int)T, bcounts, rslot);
   if (int rc = check_launch("prefill_topk_count_kernel")) return rc;
   if (int rc = mark(3)) return rc;
   prefill_scan_kernel<<<cdiv(R, kScanRoutes), 1024, 0, st>>>(a.ids, rslot, bcounts, nb, (int)T,

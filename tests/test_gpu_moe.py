@@ -124,3 +124,40 @@ def test_skewed_router_bias(dev):
     ref, (_, _, ri) = O.moe_layer(npf(h), layer, k=8, eps=EPS)
     assert np.array_equal(ids.cpu().numpy(), ri)
     assert_close(npf(out), ref, BF16_TOL, 'skewed prefill layer')
+
+
+def _bf16_up(v):
+    """The next bf16 value above each element of the bf16 tensor v (finite, nonzero)."""
+    bits = v.view(torch.int16).to(torch.int32)
+    step = torch.where(v > 0, 1, -1).to(torch.int32)
+    return (bits + step).to(torch.int16).view(torch.bfloat16)
+
+
+@pytest.mark.parametrize('mode', ['near_ties', 'all_equal'])
+def test_prefill_router_boundary(dev, mode):
+    """Prefill routing stays exact where approximate router logits cannot
+    separate experts: 32 router rows that differ from a dominant row by one
+    bf16 step in one element (exact logits equal or one bf16 step apart, so
+    the 8 winners among them are decided by the exact logits and the id
+    order), and all 256 rows equal (every expert is a candidate)."""
+    st = SyntheticMoEStack(layers=1, seed=21, device=dev, max_tokens=128)
+    w = st.router_w[0].clone()
+    if mode == 'near_ties':
+        base = (w[5].float() * 3.0).to(torch.bfloat16)
+        for i, e in enumerate(range(0, 256, 8)):
+            row = base.clone()
+            if i:
+                k = (i * 37) % 2048
+                row[k] = _bf16_up(row[k:k + 1])[0]
+            w[e] = row
+    else:
+        w[:] = w[3]
+    st.router_w[0].copy_(w)
+    h = inputs(128, 22, dev)
+    _, ids, wts = run_layer(st, h)
+    xn = O.rmsnorm(npf(h), None, EPS)
+    _, rw, ri = O.router(xn, st.layer_host(0, experts=[])['router_w'], 8)
+    assert np.array_equal(ids.cpu().numpy(), ri)
+    assert np.abs(npf(wts) - rw).max() <= 2.0 ** -8
+    if mode == 'all_equal':
+        assert (ids.cpu().numpy() == np.arange(8)).all()
