@@ -1,13 +1,16 @@
 """Benchmark: synthetic 40-layer MoE-FFN stack on one MI355X.
 
 One step = one request of the headline workload: a 4096-token prefill in two
-2048-token chunks (W8A16 grouped MFMA GEMMs) followed by 33 serial decode
-tokens (W8A8 expert GEMVs, the 40-layer decode step replayed as a HIP graph),
-over random-init int8 group-128 weights (~33.4 GB) resident in HBM.
+2048-token chunks (W8A16 grouped MFMA GEMMs; the 40-layer pass over one chunk
+replayed as a HIP graph) followed by 33 serial decode tokens (W8A8 expert
+GEMVs, the 40-layer decode step replayed as a HIP graph), over random-init
+int8 group-128 weights (~33.4 GB) resident in HBM.
 
 Prints one JSON line.  value = prefill tok/s; decode tok/s, decode HBM GB/s
-and the roofline of the dominant kernel ride along.  Per-phase kernel times
-come from HIP events recorded on the launch stream inside the timed steps.
+and the roofline of the dominant kernel ride along.  Per-kernel times come
+from HIP events recorded on the launch stream inside the timed steps, around
+one extra eager prefill chunk and one extra eager decode token per step
+(graphs cannot hold event records); those two are timed apart from tok/s.
 """
 import argparse
 import json
@@ -287,16 +290,31 @@ def main():
         torch.cuda.synchronize()
         spin_cycles = int((1 << 20) * 3.0 / max(a.elapsed_time(b), 1e-3))  # ~3 ms
 
-    pf_events = None if args.no_events else [[make_events(8) for _ in range(L)]
-                                             for _ in range(nchunks)]
+    # prefill: one 2048-token chunk through all layers, captured once as a
+    # HIP graph and replayed per chunk (the chunk is copied into its input)
+    pstatic = x[:CHUNK].clone()
+    with torch.cuda.stream(side):
+        stack.forward(pstatic.clone())
+    torch.cuda.current_stream().wait_stream(side)
+    pgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(pgraph):
+        stack.forward(pstatic)
+    # Per-kernel prefill times: one more chunk per timed step, launched
+    # eagerly with events between its kernels behind a spin kernel (as for
+    # decode), timed apart from prefill tok/s.
+    pf_events = None if args.no_events else [make_events(8) for _ in range(L)]
+    pprobe = torch.empty_like(pstatic)
 
-    def prefill(events=None):
-        out = x.clone()
+    def prefill():
         for c in range(nchunks):
-            hc = out[c * CHUNK:(c + 1) * CHUNK]
-            for l in range(L):
-                stack.layer_forward(hc, l, events=None if events is None else events[c][l])
-        return out
+            pstatic.copy_(x[c * CHUNK:(c + 1) * CHUNK])
+            pgraph.replay()
+
+    def prefill_kernel_probe():
+        pprobe.copy_(x[:CHUNK])
+        torch.cuda._sleep(3 * spin_cycles)
+        for l in range(L):
+            stack.layer_forward(pprobe, l, events=pf_events[l])
 
     def decode():
         for i in range(DECODE_TOKENS):
@@ -324,19 +342,19 @@ def main():
     for s in range(args.steps):
         m = marks[s]
         m[0].record()
-        prefill(pf_events)
+        prefill()
         m[1].record()
         decode()
         m[2].record()
         if dec_ev is not None:
             decode_kernel_probe()
         if pf_events is not None:
+            prefill_kernel_probe()
             torch.cuda.synchronize()
-            for c in range(nchunks):
-                for l in range(L):
-                    ev = pf_events[c][l]
-                    for i, p in enumerate(PREFILL_PHASES):
-                        phase_ms[p] += ev[i].elapsed_time(ev[i + 1])
+            for l in range(L):
+                ev = pf_events[l]
+                for i, p in enumerate(PREFILL_PHASES):
+                    phase_ms[p] += ev[i].elapsed_time(ev[i + 1])
             for l in range(L):
                 for j, p in enumerate(DECODE_PHASES):
                     dec_ms[p] += dec_ev[l][j].elapsed_time(dec_ev[l][j + 1])
@@ -361,7 +379,7 @@ def main():
             stack.layer_forward(hc, l, ids)
             active.append(int(torch.unique(ids).numel()))
 
-    launches_pf = steps * nchunks * L
+    launches_pf = steps * L  # prefill launches timed: the probe chunk of every request
     mean_active = float(np.mean(active))
     kernels = {}
     if pf_events is not None:
@@ -393,9 +411,10 @@ def main():
     # dominant kernel by total time within one request
     per_req = {}
     if pf_events is not None:
-        per_req['prefill_gate_up'] = phase_ms['gate_up'] / steps
-        per_req['prefill_down'] = phase_ms['down'] / steps
-        per_req['prefill_router_logits'] = phase_ms['router_logits'] / steps
+        # the probe times one chunk per request; a request has nchunks of them
+        per_req['prefill_gate_up'] = phase_ms['gate_up'] / steps * nchunks
+        per_req['prefill_down'] = phase_ms['down'] / steps * nchunks
+        per_req['prefill_router_logits'] = phase_ms['router_logits'] / steps * nchunks
         for p in DECODE_PHASES:
             per_req[p] = dec_ms[p] / steps * DECODE_TOKENS
     roofline = None
