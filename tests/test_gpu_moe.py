@@ -113,6 +113,31 @@ def test_decode_graph_replay(stack, dev):
         assert torch.equal(static, eager)
 
 
+def test_prefill_graph_replay(stack, dev):
+    """The prefill path (96 tokens, both layers) captured as a HIP graph gives
+    the eager result on every replay, with eager prefill work in between."""
+    h0 = inputs(96, 14, dev)
+    eager = h0.clone()
+    stack.forward(eager)
+    static = h0.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        stack.forward(static.clone())
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        stack.forward(static)
+    for i in range(3):
+        static.copy_(h0)
+        graph.replay()
+        torch.cuda.synchronize()
+        other = inputs(67, 15 + i, dev)
+        stack.forward(other)
+        torch.cuda.synchronize()
+        assert torch.equal(static, eager)
+
+
 def test_skewed_router_bias(dev):
     st = SyntheticMoEStack(layers=1, seed=12, device=dev, max_tokens=256,
                            router_bias=zipf_bias())
