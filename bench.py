@@ -1,8 +1,9 @@
 """Benchmark: synthetic 40-layer MoE-FFN stack on one MI355X.
 
 One step = one request of the headline workload: a 4096-token prefill in two
-2048-token chunks (W8A16 grouped MFMA GEMMs; the 40-layer pass over one chunk
-replayed as a HIP graph) followed by 33 serial decode tokens (W8A8 expert
+2048-token chunks (W8A16 grouped MFMA GEMMs; the second chunk runs one layer
+behind the first on a second stream, both 40-layer passes replayed as one HIP
+graph) followed by 33 serial decode tokens (W8A8 expert
 GEMVs, the 40-layer decode step replayed as a HIP graph), over random-init
 int8 group-128 weights (~33.4 GB) resident in HBM.
 
@@ -38,7 +39,7 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument('--gpus', type=int, default=1)
     p.add_argument('--steps', type=int, default=3)
-    p.add_argument('--warmup', type=int, default=1)
+    p.add_argument('--warmup', type=int, default=2)
     p.add_argument('--layers', type=int, default=40)
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--no-events', action='store_true',
@@ -290,25 +291,25 @@ def main():
         torch.cuda.synchronize()
         spin_cycles = int((1 << 20) * 3.0 / max(a.elapsed_time(b), 1e-3))  # ~3 ms
 
-    # prefill: one 2048-token chunk through all layers, captured once as a
-    # HIP graph and replayed per chunk (the chunk is copied into its input)
-    pstatic = x[:CHUNK].clone()
+    # prefill: both 2048-token chunks through all layers, the second chunk on
+    # a second stream one layer behind the first (MoEStack.prefill_),
+    # captured once as a HIP graph; the prompt is copied into its input
+    pstatic = x.clone()
     with torch.cuda.stream(side):
-        stack.forward(pstatic.clone())
+        stack.prefill_(pstatic.clone(), CHUNK)
     torch.cuda.current_stream().wait_stream(side)
     pgraph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(pgraph):
-        stack.forward(pstatic)
+        stack.prefill_(pstatic, CHUNK)
     # Per-kernel prefill times: one more chunk per timed step, launched
     # eagerly with events between its kernels behind a spin kernel (as for
     # decode), timed apart from prefill tok/s.
     pf_events = None if args.no_events else [make_events(8) for _ in range(L)]
-    pprobe = torch.empty_like(pstatic)
+    pprobe = torch.empty_like(x[:CHUNK])
 
     def prefill():
-        for c in range(nchunks):
-            pstatic.copy_(x[c * CHUNK:(c + 1) * CHUNK])
-            pgraph.replay()
+        pstatic.copy_(x)
+        pgraph.replay()
 
     def prefill_kernel_probe():
         pprobe.copy_(x[:CHUNK])
@@ -336,7 +337,6 @@ def main():
     marks = [make_events(3) for _ in range(args.steps)]
     phase_ms = {p: 0.0 for p in PREFILL_PHASES}
     dec_ms = {p: 0.0 for p in DECODE_PHASES}
-    t_prefill = t_decode = 0.0
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     for s in range(args.steps):
@@ -360,9 +360,10 @@ def main():
                     dec_ms[p] += dec_ev[l][j].elapsed_time(dec_ev[l][j + 1])
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    for m in marks:
-        t_prefill += m[0].elapsed_time(m[1]) / 1e3
-        t_decode += m[1].elapsed_time(m[2]) / 1e3
+    pf_steps = [m[0].elapsed_time(m[1]) for m in marks]
+    dec_steps = [m[1].elapsed_time(m[2]) for m in marks]
+    t_prefill = sum(pf_steps) / 1e3
+    t_decode = sum(dec_steps) / 1e3
     steps = args.steps
     log(f'timed {steps} steps: {wall:.3f} s')
     prefill_tok_s = steps * PREFILL_TOKENS / t_prefill
@@ -443,8 +444,12 @@ def main():
                                f'W8A16) + 33 decode tokens (W8A8 experts), 256 experts top-8 + '
                                f'shared, hidden 2048, intermediate 512',
                    'layers': L, 'prefill_tokens': PREFILL_TOKENS, 'chunk': CHUNK,
+                   'prefill_schedule': 'chunk 2 enters layer l once chunk 1 has left layer '
+                                       'l-1 (second stream); one HIP graph',
                    'decode_tokens': DECODE_TOKENS, 'bank_gb': round(stack.bank_bytes() / 1e9, 2)},
         'prefill_tok_s': round(prefill_tok_s, 1),
+        'prefill_ms_steps': [round(t, 3) for t in pf_steps],
+        'decode_ms_steps': [round(t, 3) for t in dec_steps],
         'decode_tok_s': round(decode_tok_s, 1),
         'decode_hbm_gbs': round(decode_gbs, 1),
         'decode_hbm_frac': round(decode_gbs / HBM_PEAK_GBS, 4),

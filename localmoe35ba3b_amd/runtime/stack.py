@@ -86,6 +86,7 @@ class MoEStack:
         self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         _lib.call('lm_moe_workspace_init', self.workspace.data_ptr(), nbytes, _lib.stream(dev))
         self._structs = [self._layer_struct(l) for l in range(layers)]
+        self._side = self._side_ws = None  # second stream and workspace of prefill_
 
     # ------------------------------------------------------------------ views
     def bank_bytes(self):
@@ -116,8 +117,16 @@ class MoEStack:
                 self.dn_s[l, :self.E]]
 
     # ------------------------------------------------------------------ forward
-    def layer_forward(self, h, l, ids_out=None, weights_out=None, events=None):
-        """h bf16 [T, H] updated in place: h = h + block(rmsnorm(h))."""
+    def new_workspace(self):
+        """Another fused-layer workspace of this stack's size, for a chunk that
+        runs concurrently with the one using `self.workspace`."""
+        ws = torch.empty_like(self.workspace)
+        _lib.call('lm_moe_workspace_init', ws.data_ptr(), ws.numel(), _lib.stream(self.device))
+        return ws
+
+    def layer_forward(self, h, l, ids_out=None, weights_out=None, events=None, workspace=None):
+        """h bf16 [T, H] updated in place: h = h + block(rmsnorm(h)).  Chunks
+        in flight at the same time need workspaces of their own."""
         if h.dtype != torch.bfloat16 or not h.is_contiguous() or h.shape[-1] != self.H:
             raise ValueError('expected contiguous bf16 [tokens, 2048] hidden states')
         tokens = h.shape[0]
@@ -126,10 +135,10 @@ class MoEStack:
         ev = None
         if events is not None:
             ev = (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
+        ws = self.workspace if workspace is None else workspace
         _lib.call('lm_moe_layer_forward', ctypes.byref(self._structs[l]), h.data_ptr(), tokens,
-                  self.H, self.I, self.E, self.K, EPS, self.workspace.data_ptr(),
-                  self.workspace.numel(), _lib.ptr(ids_out), _lib.ptr(weights_out), ev,
-                  _lib.stream(h.device))
+                  self.H, self.I, self.E, self.K, EPS, ws.data_ptr(), ws.numel(),
+                  _lib.ptr(ids_out), _lib.ptr(weights_out), ev, _lib.stream(h.device))
         return h
 
     def forward(self, h, layers=None):
@@ -137,12 +146,53 @@ class MoEStack:
             self.layer_forward(h, l)
         return h
 
-    def prefill(self, x, chunk=2048):
+    def prefill(self, x, chunk=2048, overlap=True):
         """Runs all layers over x [T, H] in chunks of `chunk` tokens; returns h."""
         out = x.clone()
-        for c0 in range(0, x.shape[0], chunk):
-            self.forward(out[c0:c0 + chunk])
+        self.prefill_(out, chunk, overlap)
         return out
+
+    def prefill_(self, h, chunk=2048, overlap=True):
+        """In-place chunked prefill of h [T, H], as the reference's chunked
+        profile runs the model over consecutive `chunk`-token slices of the
+        prompt (generation.py:39-42).
+
+        With overlap, consecutive chunks alternate between the current stream
+        and a second stream with a workspace of its own, and chunk c enters
+        layer l as soon as chunk c-1 has left layer l-1.  That is the order a
+        model with attention between its MoE blocks allows: chunk c's layer-l
+        attention reads the keys and values chunk c-1 made from its layer-l
+        input.  One chunk's latency-bound routing kernels then run beside the
+        other's grouped GEMMs.  Every chunk computes exactly what it computes
+        alone, so the result is bit-identical to overlap=False.  The schedule
+        is stream-ordered and HIP-graph capturable.
+        """
+        starts = list(range(0, h.shape[0], chunk))
+        if not overlap or len(starts) == 1:
+            for c0 in starts:
+                self.forward(h[c0:c0 + chunk])
+            return h
+        if self._side is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError('run prefill_ once outside graph capture first: the second '
+                                   'workspace must not come from the graph pool')
+            self._side = torch.cuda.Stream(self.device)
+            self._side_ws = self.new_workspace()
+        cur = torch.cuda.current_stream(self.device)
+        streams, spaces = (cur, self._side), (self.workspace, self._side_ws)
+        self._side.wait_stream(cur)
+        done = [[torch.cuda.Event() for _ in range(self.L)] for _ in starts]
+        for l in range(self.L):
+            for c, c0 in enumerate(starts):
+                st = streams[c % 2]
+                with torch.cuda.stream(st):
+                    if c and l:
+                        st.wait_event(done[c - 1][l - 1])
+                    self.layer_forward(h[c0:c0 + chunk], l, workspace=spaces[c % 2])
+                    done[c][l].record(st)
+        cur.wait_stream(self._side)
+        self._done_events = done  # kept alive until the next call
+        return h
 
     # ------------------------------------------------------------------ oracle views
     def layer_host(self, l, experts=None):

@@ -138,6 +138,29 @@ def test_prefill_graph_replay(stack, dev):
         assert torch.equal(static, eager)
 
 
+@pytest.mark.parametrize('tokens,chunk', [(250, 96), (4096, 2048)])
+def test_overlapped_prefill(stack, dev, tokens, chunk):
+    """Chunks overlapped on two streams (chunk c enters layer l once chunk
+    c-1 has left layer l-1) equal chunks run one after the other, eagerly
+    and as a HIP graph replayed with eager work in between; 250 tokens in
+    chunks of 96 give three chunks, the last one ragged."""
+    h0 = inputs(tokens, 21, dev)
+    serial = stack.prefill(h0, chunk=chunk, overlap=False)
+    assert torch.equal(stack.prefill(h0, chunk=chunk), serial)
+    static = h0.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        stack.prefill_(static, chunk)
+    for i in range(3):
+        static.copy_(h0)
+        graph.replay()
+        torch.cuda.synchronize()
+        other = inputs(67, 30 + i, dev)
+        stack.forward(other)
+        torch.cuda.synchronize()
+        assert torch.equal(static, serial), f'replay {i}'
+
+
 def test_skewed_router_bias(dev):
     st = SyntheticMoEStack(layers=1, seed=12, device=dev, max_tokens=256,
                            router_bias=zipf_bias())
