@@ -105,6 +105,17 @@ int lm_w8a8_group_partials(const int8_t *xq, const int8_t *wq, int32_t *p,
 int lm_w8a8_linear(const void *x, const int8_t *q, const float *s, void *y,
                    int64_t m, int64_t n, int64_t k, int swiglu, void *stream);
 
+/* W8A8 MFMA GEMM for any number of rows (int8 x int8 -> int32 MFMA with
+ * the per-group fp32 rescale), on rows already quantized by
+ * lm_act_quant_g128: xq int8 [m, k], xs fp32 [m, k/128]; weights q int8
+ * [n, k], s fp32 [n, k/128]; y bf16 [m, n], or [m, n/2] with swiglu as in
+ * lm_w8a8_linear.  Replaces w8a8._linear (w8a8.py:25-41) applied to every
+ * row rather than row 0 only: exact int32 group partials, then
+ * acc = acc + (f32(p) * xs) * ws in ascending group order, unfused, so the
+ * output is bit-identical to the reference's for each row. */
+int lm_w8a8_gemm(const int8_t *xq, const float *xs, const int8_t *q, const float *s,
+                 void *y, int64_t m, int64_t n, int64_t k, int swiglu, void *stream);
+
 /* bf16 SwiGLU glue: h[r, c] = bf16(bf16(silu(gu[r, c])) * gu[r, half + c]).
  * Replaces `gate, up = gu.chunk(2, -1); silu(gate) * up`
  * (int8.py:182-184, prefill.py:77-78, gpu_routes.py:74-75). */

@@ -32,6 +32,7 @@ SIGNATURES = {
     'lm_w8a8_grouped_linear': (I32, [P, P, P, I64, I64, I64, I32, I32, P]),
     'lm_w8a8_group_partials': (I32, [P, P, P, I64, I64, I64, P]),
     'lm_w8a8_linear': (I32, [P, P, P, P, I64, I64, I64, I32, P]),
+    'lm_w8a8_gemm': (I32, [P, P, P, P, P, I64, I64, I64, I32, P]),
     'lm_swiglu': (I32, [P, P, I64, I64, P]),
     'lm_ordered_reduce': (I32, [P, P, P, I32, P, I64, I64, P]),
     'lm_routed_reduce': (I32, [P, P, P, P, I32, P, I64, I64, I64, P]),

@@ -11,12 +11,14 @@
 // MFMA (the reference rounds the dequantized weight to the activation dtype
 // before the MMA, int8.py:21), so the MFMA consumes bit-identical operands
 // to the reference's tl.dot; only the fp32 summation order differs.
-//   w8a16_mfma_kernel    dense and generic: 256 threads, BM x 128 tile, K in
-//                        64-wide stages, weights dequantized into LDS.
+//   w8a16_mfma_kernel    dense and generic (fp16 rows, other K): 256 threads,
+//                        BM x 128 tile, K in 64-wide stages, weights
+//                        dequantized into LDS.
 //   grouped_mfma_kernel  routed, any K, up to 128-row tiles (large_tile).
-//   grouped_rb_kernel    routed, the model's K (2048 gate_up, 512 down) and
-//                        tiles of up to 96 rows: weights streamed straight
-//                        into registers and dequantized there.
+//   grouped_rb_kernel    routed, and dense bf16, at the model's K (2048
+//                        gate_up, 512 down) in tiles of up to 96 rows:
+//                        weights streamed straight into registers and
+//                        dequantized there.
 // In SwiGLU mode a tile's columns pair every gate column with its up partner
 // in the same lane.
 #include "internal.hpp"
@@ -718,9 +720,15 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
   __shared__ __align__(16) unsigned char smem[3 * BM * 128 * HL + SC_BYTES];
   int mt, nt;
   if (!xcd_tile(a, mt, nt)) return;
-  const int64_t e = a.table[mt * 3];
-  const int64_t start = a.table[mt * 3 + 1];
-  const int64_t stop = a.table[mt * 3 + 2];
+  int64_t e = 0, start, stop;
+  if (a.table) {
+    e = a.table[mt * 3];
+    start = a.table[mt * 3 + 1];
+    stop = a.table[mt * 3 + 2];
+  } else {  // dense: row tile mt of an [M, K] matrix
+    start = (int64_t)mt * BM;
+    stop = a.M;
+  }
   if (start >= stop) return;
   const int rows = (int)min((int64_t)a.tile_rows, stop - start);
   static_assert(BM == 96, "row-count dispatch below covers 96-row tiles");
@@ -810,6 +818,13 @@ int w8a16_gemm_dense(const void *x, const int8_t *q, const float *s, void *y, in
   a.N = (int)n;
   a.K = (int)k;
   (void)large_tile;
+  // bf16 rows at the model's K: the register-streamed kernel over 96-row
+  // tiles of the dense matrix (no tile table), faster than the LDS-dequant
+  // kernel because each wave dequantizes only its own columns' weights.
+  if (dtype == LM_BF16 && (k == 2048 || k == 512)) {
+    a.tile_rows = 96;
+    return launch_grouped<false, false>(a, cdiv(m, 96), st);
+  }
   const unsigned mt = cdiv(m, 128);
   if (dtype == LM_BF16) return launch_gemm<BF16, 128, 2, false, false, true>(a, mt, st);
   return launch_gemm<FP16, 128, 2, false, false, true>(a, mt, st);

@@ -4,7 +4,9 @@ quantize          per-row, per-128-group dynamic int8 activation quantization
                   (w8a8.py:8-22): s = max(amax, 1e-10) * fl32(1/127), q = rint(x / s)
 grouped_linear    grouped W8A8 GEMV (w8a8.py:25-48): exact int32 dot per group,
                   acc = acc + (f32(p) * xs) * ws in ascending group order, no FMA
-linear            dense W8A8 linear for 1..8 rows with optional fused SwiGLU
+linear            dense W8A8 linear with optional fused SwiGLU (GEMV up to 8 rows,
+                  int8 MFMA GEMM beyond)
+gemm              the int8 MFMA GEMM on quantized rows
 group_partials    the exact int32 per-group partials the GEMV accumulates
 
 Swapping `int8.grouped_linear = w8a8.grouped_linear` switches Int8Experts'
@@ -51,17 +53,44 @@ def grouped_gemv(q, s, table, experts, n, field, shared):
 
 
 def linear(x, q, scale, swiglu=False):
-    """Dense W8A8 linear for 1..8 bf16 rows: bf16 [M, N] or, with swiglu, [M, N/2]."""
+    """Dense W8A8 linear of bf16 rows: bf16 [M, N] or, with swiglu, [M, N/2].
+    Up to 8 rows run as one fused quantize + GEMV launch; more rows are
+    quantized (quantize) and multiplied by the int8 MFMA GEMM (gemm)."""
     x = x.contiguous()
     if not x.is_cuda or x.ndim != 2 or x.dtype != torch.bfloat16:
         raise ValueError('Expected CUDA rows with K divisible by 128')
     n, k = q.shape
     if k % 128 or x.shape[-1] != k or tuple(scale.shape) != (n, k // 128):
         raise ValueError('Invalid INT8 group geometry')
+    if x.shape[0] > 8:
+        xq, xs = quantize(x)
+        return gemm(xq, xs, q, scale, swiglu)
     out = torch.empty((x.shape[0], n // 2 if swiglu else n), device=x.device, dtype=x.dtype)
     _lib.call('lm_w8a8_linear', x.data_ptr(), q.contiguous().data_ptr(),
               scale.contiguous().data_ptr(), out.data_ptr(), x.shape[0], n, k, int(bool(swiglu)),
               _lib.stream(x.device))
+    return out
+
+
+def gemm(xq, xs, q, scale, swiglu=False):
+    """W8A8 GEMM of quantized rows (xq int8 [M, K], xs fp32 [M, K/128], as
+    returned by quantize) with int8 weights q [N, K] and fp32 group scales
+    [N, K/128]: w8a8._linear (w8a8.py:25-41) for every row, int32 MFMA group
+    partials and the unfused fp32 rescale in ascending group order; bf16
+    [M, N] or, with swiglu, [M, N/2]."""
+    if not (xq.is_cuda and q.is_cuda) or xq.dtype != torch.int8 or q.dtype != torch.int8:
+        raise ValueError('Expected CUDA int8 rows and weights')
+    m, k = xq.shape
+    n = q.shape[0]
+    if (k % 128 or q.shape[1] != k or tuple(scale.shape) != (n, k // 128)
+            or tuple(xs.shape) != (m, k // 128)):
+        raise ValueError('Invalid INT8 group geometry')
+    if swiglu and n % 2:
+        raise ValueError('SwiGLU needs an even number of weight rows')
+    out = torch.empty((m, n // 2 if swiglu else n), device=xq.device, dtype=torch.bfloat16)
+    _lib.call('lm_w8a8_gemm', xq.contiguous().data_ptr(), xs.contiguous().data_ptr(),
+              q.contiguous().data_ptr(), scale.contiguous().data_ptr(), out.data_ptr(), m, n, k,
+              int(bool(swiglu)), _lib.stream(xq.device))
     return out
 
 

@@ -51,6 +51,12 @@ def test_invalid_geometry_rejected_before_launch():
     assert lib.lm_router_topk(None, None, None, None, None, None, 1, 512, 2048, 8,
                               None) == _lib.LM_EINVAL
     assert lib.lm_w8a8_linear(None, None, None, None, 9, 64, 128, 0, None) == _lib.LM_EINVAL
+    assert lib.lm_w8a8_gemm(None, None, None, None, None, 9, 64, 100, 0, None) == _lib.LM_EINVAL
+    assert b'Invalid INT8 group geometry' in lib.lm_last_error()
+    assert lib.lm_w8a8_gemm(None, None, None, None, None, 9, 63, 128, 1, None) == _lib.LM_EINVAL
+    assert lib.lm_w8a8_gemm(None, None, None, None, None, 9, 64, 128, 0, None) == _lib.LM_EINVAL
+    assert b'null pointer' in lib.lm_last_error()
+    assert lib.lm_w8a8_gemm(None, None, None, None, None, 0, 64, 128, 0, None) == _lib.LM_OK
 
 
 def test_status_maps_to_reference_exceptions():
@@ -66,6 +72,8 @@ def test_python_wrappers_validate_like_reference():
         int8.linear(x, q, s)
     with pytest.raises(ValueError, match='Expected CUDA rows with K divisible by 128'):
         w8a8.quantize(x)
+    with pytest.raises(ValueError, match='Expected CUDA int8 rows and weights'):
+        w8a8.gemm(q[:2], s[:2], q, s)
     with pytest.raises(ValueError, match='Expected contiguous CUDA'):
         gpu_routes.plan(torch.zeros(2, 8, dtype=torch.int64), 256, 16)
     with pytest.raises(ValueError, match='Expected nonempty CPU'):
