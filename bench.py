@@ -24,6 +24,7 @@ import torch
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
+INT8_PEAK_TOPS = 5033.2
 PREFILL_TOKENS, CHUNK, DECODE_TOKENS = 4096, 2048, 33
 H, I, E, K = 2048, 512, 256, 8
 GU_EXPERT_BYTES = 2 * I * H + 2 * I * (H // 128) * 4        # 2,162,688
@@ -164,6 +165,76 @@ def lm_head_probe(dev, reps=20):
     return {'avg_us': round(us, 2), 'launches': reps, 'bytes_per_launch': nbytes,
             'gbs': round(nbytes / us / 1e3, 1), 'hbm_frac': round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
             'shape': f'[1, {k}] x [{n}, {k}] int8 g128'}
+
+
+def isolated_probe(dev, spin_cycles, reps=32):
+    """The single-kernel configurations of the workload, each timed on its own
+    with per-launch HIP events behind a spin kernel that holds the stream
+    until every launch is queued (so the events see the launches back to
+    back, not the host's launch gaps); medians over the launches.  The
+    HBM-bound cases rotate over weight copies of at least 512 MB in total,
+    twice the 256 MB Infinity Cache, so every launch streams its weights from
+    HBM.  Covers the dense W8A16 linear [4096, 2048] at 1 and 2048 rows, the
+    W8A8 gate_up + SwiGLU [1024, 2048] at 1, 4 and 8 rows, and the int8 MFMA
+    W8A8 GEMM at 2048 x 4096 x 2048 (the one-token MoE layer is the stack's
+    decode layer, timed per kernel in the request)."""
+    from localmoe35ba3b_amd.convert import quantize_g128
+    from localmoe35ba3b_amd.operators import int8, w8a8
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+
+    def run(fn, n):  # spin_cycles: about 12 ms, longer than queueing n launches takes
+        fn(0)
+        torch.cuda.synchronize()
+        ev = make_events(n + 1)
+        torch.cuda._sleep(spin_cycles)
+        ev[0].record()
+        for i in range(n):
+            fn(i)
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        return sorted(ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(n))[n // 2]
+
+    def hbm(us, nbytes, shape):
+        return {'avg_us': round(us, 2), 'bytes_per_launch': nbytes,
+                'gbs': round(nbytes / us / 1e3, 1),
+                'hbm_frac': round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), 'shape': shape}
+
+    out = {}
+    w = torch.randn((4096, H), generator=gen, device=dev) * 0.02
+    q, s = quantize_g128(w)
+    del w
+    pool = 64  # 64 x 8.66 MB
+    qp = q.unsqueeze(0).expand(pool, -1, -1).contiguous()
+    sp = s.unsqueeze(0).expand(pool, -1, -1).contiguous()
+    x1 = torch.randn((1, H), generator=gen, device=dev).to(torch.bfloat16)
+    us = run(lambda i: int8.linear(x1, qp[i % pool], sp[i % pool]), reps)
+    out['w8a16_linear_m1'] = hbm(us, 4096 * H + 4096 * (H // 128) * 4 + H * 2 + 4096 * 2,
+                                 '[1, 2048] x [4096, 2048] int8 g128')
+    del qp, sp
+    x2 = torch.randn((CHUNK, H), generator=gen, device=dev).to(torch.bfloat16)
+    flops = 2.0 * CHUNK * 4096 * H
+    us = run(lambda i: int8.linear(x2, q, s), 8)
+    out['w8a16_linear_m2048'] = {'avg_us': round(us, 2), 'tflops': round(flops / us / 1e6, 1),
+                                 'mfma_frac': round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                                 'shape': '[2048, 2048] x [4096, 2048] int8 g128'}
+    xq, xs = w8a8.quantize(x2)
+    us = run(lambda i: w8a8.gemm(xq, xs, q, s), 8)
+    out['w8a8_gemm_m2048'] = {'avg_us': round(us, 2), 'tops': round(flops / us / 1e6, 1),
+                              'int8_mfma_frac': round(flops / us / 1e6 / INT8_PEAK_TOPS, 4),
+                              'shape': '[2048, 2048] x [4096, 2048] int8 g128 (rows pre-quantized)'}
+    w = torch.randn((2 * I, H), generator=gen, device=dev) * 0.02
+    q2, s2 = quantize_g128(w)
+    del w, q, s
+    pool = 256  # 256 x 2.16 MB
+    q2p = q2.unsqueeze(0).expand(pool, -1, -1).contiguous()
+    s2p = s2.unsqueeze(0).expand(pool, -1, -1).contiguous()
+    for m in (1, 4, 8):
+        xm = torch.randn((m, H), generator=gen, device=dev).to(torch.bfloat16)
+        us = run(lambda i: w8a8.linear(xm, q2p[i % pool], s2p[i % pool], swiglu=True), reps)
+        out[f'w8a8_gate_up_swiglu_m{m}'] = hbm(
+            us, GU_EXPERT_BYTES + H * 2 * m + I * 2 * m, f'[{m}, 2048] x [1024, 2048] int8 g128')
+    return out
 
 
 def skewed_prefill_probe(dev, reps=5):
@@ -430,6 +501,7 @@ def main():
 
     kernels['lm_head_gemv'] = lm_head_probe(dev)  # after the timed steps, timed on its own
     skewed = None if args.no_events else skewed_prefill_probe(dev)
+    isolated = None if args.no_events else isolated_probe(dev, 4 * spin_cycles)
 
     cores = min(16, os.cpu_count() or 1)
     cpu = None if args.no_cpu_baseline else cpu_baseline(stack, x, dec_in, cores)
@@ -458,6 +530,7 @@ def main():
         'roofline': roofline,
         'kernels': kernels,
         'prefill_zipf_layer': skewed,
+        'isolated_kernels': isolated,
         'cpu_baseline': cpu,
         'build_s': round(t_build, 1),
     }

@@ -108,14 +108,21 @@ __global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
   const int8_t *q = rv.q;
   auto row_ptr = [&](int r) { return q + (int64_t)rv.map(r) * K; };
   const int sub = threadIdx.x & 7;
+  // All MT rows are computed branch-free (rows past M read LDS rows that are
+  // never stored back; only the stores are guarded), so the dot-product
+  // chains of the rows interleave instead of running one basic block at a time.
   stream_rows<kGemvLoads>(rv.rvalid, G, row_ptr, [&](u32x4 w, int r, int g, int f, bool ok) {
+    u32x4 xv[MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      if (m < M) {
-        const u32x4 xv = *reinterpret_cast<const u32x4 *>(xq + m * K + g * 128 + sub * 16);
-        const int p = octet_sum_i32(dot16_i8(w, xv));
-        if (ok && sub == 0) part[m * RG + f] = p;
-      }
+    for (int m = 0; m < MT; ++m)
+      xv[m] = *reinterpret_cast<const u32x4 *>(xq + m * K + g * 128 + sub * 16);
+    int p[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) p[m] = octet_sum_i32(dot16_i8(w, xv[m]));
+    if (ok && sub == 0) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        if (m < M) part[m * RG + f] = p[m];
     }
   });
   __syncthreads();
@@ -174,26 +181,32 @@ __global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_kernel(GemvArgs a) {
   const int8_t *q = rv.q;
   auto row_ptr = [&](int r) { return q + (int64_t)rv.map(r) * K; };
   const int sub = threadIdx.x & 7;
+  // All MT rows computed branch-free, stores guarded (as in w8a8_gemv_kernel).
   stream_rows<kGemvLoads>(rv.rvalid, G, row_ptr, [&](u32x4 w, int r, int g, int f, bool ok) {
-    uint32_t wd[8];
-    dequant16<T>(w, ok ? ws[f] : 0.0f, wd);
+    const float sc = ok ? ws[f] : 0.0f;
+    u32x4 x0[MT], x1[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      if (m < M) {
-        const uint16_t *xp = xl + m * K + g * 128 + sub * 16;
-        const u32x4 x0 = *reinterpret_cast<const u32x4 *>(xp);
-        const u32x4 x1 = *reinterpret_cast<const u32x4 *>(xp + 8);
-        const float p = octet_sum_f32(dot16_w16<T>(wd, x0, x1));
-        if (ok && sub == 0) part[m * RG + f] = p;
-      }
+      const uint16_t *xp = xl + m * K + g * 128 + sub * 16;
+      x0[m] = *reinterpret_cast<const u32x4 *>(xp);
+      x1[m] = *reinterpret_cast<const u32x4 *>(xp + 8);
+    }
+    uint32_t wd[8];
+    dequant16<T>(w, sc, wd);
+    float p[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) p[m] = octet_sum_f32(dot16_w16<T>(wd, x0[m], x1[m]));
+    if (ok && sub == 0) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        if (m < M) part[m * RG + f] = p[m];
     }
   });
   __syncthreads();
 
   for (int i = threadIdx.x; i < M * rv.rvalid; i += blockDim.x) {
     const int m = i / rv.rvalid, t = i - m * rv.rvalid;
-    float acc = 0.0f;
-    for (int g = 0; g < G; ++g) acc += part[m * RG + t * G + g];
+    const float acc = ordered_sum8(part + m * RG + t * G, G);
     a.y[(int64_t)(rv.yrow + m) * a.ldy + rv.n0 + t] = T::from_f32(acc);
   }
 }

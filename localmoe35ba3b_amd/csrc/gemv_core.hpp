@@ -133,22 +133,45 @@ __device__ __forceinline__ void quantize_rows_to_lds(const uint16_t *x, int64_t 
   const int nhalf = blockDim.x >> 5;
   const int l = threadIdx.x & 31;
   const float inv127 = (float)(1.0 / 127.0);
-  for (int job = half; job < rows * G; job += nhalf) {
-    const int m = job / G;
-    const int g = job - m * G;
-    const uint2 raw = *reinterpret_cast<const uint2 *>(x + m * ldx + g * 128 + l * 4);
-    float v[4] = {T::to_f32(raw.x & 0xFFFFu), T::to_f32(raw.x >> 16), T::to_f32(raw.y & 0xFFFFu),
-                  T::to_f32(raw.y >> 16)};
-    float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  // Jobs (row m, group g) in batches of B per half-wave.  Every load of a
+  // batch is issued before the first is used, and the jobs are computed
+  // branch-free (jobs past the end redo the last one; only the stores are
+  // guarded), so their dependency chains interleave: a batch costs about one
+  // load latency, not one per job.  The group absmax is four DPP steps inside
+  // each 16-lane row and one shuffle across the two rows of the half-wave.
+  constexpr int B = 8;
+  const int jobs = rows * G;
+  for (int base = half; base < jobs; base += nhalf * B) {
+    uint2 raw[B];
 #pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
-    const float sc = fmaxf(a, 1e-10f) * inv127;
-    uint32_t packed = 0;
+    for (int u = 0; u < B; ++u) {
+      const int job = min(base + u * nhalf, jobs - 1);
+      const int m = job / G, g = job - (job / G) * G;
+      raw[u] = *reinterpret_cast<const uint2 *>(x + m * ldx + g * 128 + l * 4);
+    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[i] / sc)) << (8 * i);
-    *reinterpret_cast<uint32_t *>(xq + m * K + g * 128 + l * 4) = packed;
-    if (l == 0) xs[m * G + g] = sc;
+    for (int u = 0; u < B; ++u) {
+      const int jr = base + u * nhalf;
+      const int job = min(jr, jobs - 1);
+      const int m = job / G, g = job - (job / G) * G;
+      float v[4] = {T::to_f32(raw[u].x & 0xFFFFu), T::to_f32(raw[u].x >> 16),
+                    T::to_f32(raw[u].y & 0xFFFFu), T::to_f32(raw[u].y >> 16)};
+      float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+      a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0xB1, 0xF, 0xF, false)));
+      a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x4E, 0xF, 0xF, false)));
+      a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x141, 0xF, 0xF, false)));
+      a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x140, 0xF, 0xF, false)));
+      a = fmaxf(a, __shfl_xor(a, 16, 64));
+      const float sc = fmaxf(a, 1e-10f) * inv127;
+      uint32_t packed = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[i] / sc)) << (8 * i);
+      if (jr < jobs) {
+        *reinterpret_cast<uint32_t *>(xq + m * K + g * 128 + l * 4) = packed;
+        if (l == 0) xs[m * G + g] = sc;
+      }
+    }
   }
 }
 
@@ -179,10 +202,35 @@ __device__ __forceinline__ float dot16_w16(const uint32_t wd[8], u32x4 x0, u32x4
 
 // The W8A8 reference epilogue over one row's group partials (w8a8.py:40):
 // acc = acc + (float(p_g) * xs_g) * ws_g for g ascending, no FMA.
+// The terms of eight groups are formed together (their LDS reads in flight
+// at once) and then added in ascending order, which leaves the sum unchanged.
 __device__ __forceinline__ float w8a8_epilogue(const int *p, const float *xs, const float *ws,
                                                int G) {
   float acc = 0.0f;
-  for (int g = 0; g < G; ++g) acc = add_rn(acc, mul_rn(mul_rn((float)p[g], xs[g]), ws[g]));
+  int g = 0;
+  for (; g + 8 <= G; g += 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = mul_rn(mul_rn((float)p[g + u], xs[g + u]), ws[g + u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = add_rn(acc, t[u]);
+  }
+  for (; g < G; ++g) acc = add_rn(acc, mul_rn(mul_rn((float)p[g], xs[g]), ws[g]));
+  return acc;
+}
+
+// Ascending-order fp32 sum of G values, eight reads in flight at a time.
+__device__ __forceinline__ float ordered_sum8(const float *v, int G) {
+  float acc = 0.0f;
+  int g = 0;
+  for (; g + 8 <= G; g += 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = v[g + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += t[u];
+  }
+  for (; g < G; ++g) acc += v[g];
   return acc;
 }
 
