@@ -83,35 +83,13 @@ __global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
   float *ws = xs + MT * G;
   int *part = reinterpret_cast<int *>(ws + a.RB * G);
   const int RG = a.RB * G;
-
-  // Activations: quantize bf16 rows, or copy pre-quantized rows.
-  if constexpr (QUANT) {
-    quantize_rows_to_lds<BF16>(a.x + (int64_t)rv.xrow * a.ldx, a.ldx, M, K, xq, xs);
-  } else {
-    for (int i = threadIdx.x; i < M * K / 16; i += blockDim.x) {
-      const int m = (i * 16) / K, c = (i * 16) - m * K;
-      *reinterpret_cast<u32x4 *>(xq + m * K + c) =
-          ldg16(a.xq + (int64_t)(rv.xrow + m) * K + c);
-    }
-    if (a.xs)
-      for (int i = threadIdx.x; i < M * G; i += blockDim.x)
-        xs[i] = a.xs[(int64_t)(rv.xrow + i / G) * G + i % G];
-  }
-  if constexpr (!PARTIALS) {
-    for (int i = threadIdx.x; i < rv.rvalid * G; i += blockDim.x) {
-      const int r = i / G, g = i - r * G;
-      ws[i] = rv.s[(int64_t)rv.map(r) * G + g];
-    }
-  }
-  __syncthreads();
-
   const int8_t *q = rv.q;
   auto row_ptr = [&](int r) { return q + (int64_t)rv.map(r) * K; };
   const int sub = threadIdx.x & 7;
   // All MT rows are computed branch-free (rows past M read LDS rows that are
   // never stored back; only the stores are guarded), so the dot-product
   // chains of the rows interleave instead of running one basic block at a time.
-  stream_rows<kGemvLoads>(rv.rvalid, G, row_ptr, [&](u32x4 w, int r, int g, int f, bool ok) {
+  auto body = [&](u32x4 w, int r, int g, int f, bool ok) {
     u32x4 xv[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m)
@@ -124,8 +102,61 @@ __global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
       for (int m = 0; m < MT; ++m)
         if (m < M) part[m * RG + f] = p[m];
     }
-  });
-  __syncthreads();
+  };
+
+  // One batch: when the block's weights fit one RowLoads batch and its
+  // activations one register stage, the activations and scales are requested
+  // first, the weights next, and the activations are staged in LDS only then,
+  // so their wait does not include the weights: the two load latencies overlap.
+  constexpr int QJ = 2 * MT, XN = MT;
+  const int th = threadIdx.x;
+  if (rv.rvalid * G <= kGemvLoads * 8 * (kGemvThreads / 64) && M * G <= kGemvThreads &&
+      (QUANT ? M * G <= QJ * (kGemvThreads / 32) : M * K <= XN * 16 * kGemvThreads)) {
+    QuantStage<BF16, QJ> qst;
+    RowStage<XN> cst;
+    if constexpr (QUANT)
+      qst.load(a.x + (int64_t)rv.xrow * a.ldx, a.ldx, M, K);
+    else
+      cst.load(reinterpret_cast<const unsigned char *>(a.xq + (int64_t)rv.xrow * K), K, M, K);
+    const int ti = min(th, M * G - 1);
+    const float xsv = (!QUANT && a.xs) ? a.xs[(int64_t)(rv.xrow + ti / G) * G + ti % G] : 0.0f;
+    const int tw = min(th, rv.rvalid * G - 1);
+    const float wsv = PARTIALS ? 0.0f : rv.s[(int64_t)rv.map(tw / G) * G + tw % G];
+    RowLoads<kGemvLoads> L;
+    L.issue(rv.rvalid, G, row_ptr);
+    if constexpr (QUANT)
+      qst.store(K, xq, xs);
+    else
+      cst.store(reinterpret_cast<unsigned char *>(xq));
+    if (!QUANT && a.xs && th < M * G) xs[th] = xsv;
+    if (!PARTIALS && th < rv.rvalid * G) ws[th] = wsv;
+    __syncthreads();
+    L.consume(body);
+    __syncthreads();
+  } else {
+    // Activations: quantize bf16 rows, or copy pre-quantized rows.
+    if constexpr (QUANT) {
+      quantize_rows_to_lds<BF16>(a.x + (int64_t)rv.xrow * a.ldx, a.ldx, M, K, xq, xs);
+    } else {
+      for (int i = threadIdx.x; i < M * K / 16; i += blockDim.x) {
+        const int m = (i * 16) / K, c = (i * 16) - m * K;
+        *reinterpret_cast<u32x4 *>(xq + m * K + c) =
+            ldg16(a.xq + (int64_t)(rv.xrow + m) * K + c);
+      }
+      if (a.xs)
+        for (int i = threadIdx.x; i < M * G; i += blockDim.x)
+          xs[i] = a.xs[(int64_t)(rv.xrow + i / G) * G + i % G];
+    }
+    if constexpr (!PARTIALS) {
+      for (int i = threadIdx.x; i < rv.rvalid * G; i += blockDim.x) {
+        const int r = i / G, g = i - r * G;
+        ws[i] = rv.s[(int64_t)rv.map(r) * G + g];
+      }
+    }
+    __syncthreads();
+    stream_rows<kGemvLoads>(rv.rvalid, G, row_ptr, body);
+    __syncthreads();
+  }
 
   if constexpr (PARTIALS) {
     for (int i = threadIdx.x; i < M * rv.rvalid * G; i += blockDim.x) {
@@ -167,22 +198,11 @@ __global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_kernel(GemvArgs a) {
   float *ws = reinterpret_cast<float *>(smem + MT * K * 2);
   float *part = ws + a.RB * G;
   const int RG = a.RB * G;
-
-  for (int i = threadIdx.x; i < M * K / 8; i += blockDim.x) {
-    const int m = (i * 8) / K, c = (i * 8) - m * K;
-    *reinterpret_cast<u32x4 *>(xl + m * K + c) = ldg16(a.x + (int64_t)(rv.xrow + m) * a.ldx + c);
-  }
-  for (int i = threadIdx.x; i < rv.rvalid * G; i += blockDim.x) {
-    const int r = i / G, g = i - r * G;
-    ws[i] = rv.s[(int64_t)rv.map(r) * G + g];
-  }
-  __syncthreads();
-
   const int8_t *q = rv.q;
   auto row_ptr = [&](int r) { return q + (int64_t)rv.map(r) * K; };
   const int sub = threadIdx.x & 7;
   // All MT rows computed branch-free, stores guarded (as in w8a8_gemv_kernel).
-  stream_rows<kGemvLoads>(rv.rvalid, G, row_ptr, [&](u32x4 w, int r, int g, int f, bool ok) {
+  auto body = [&](u32x4 w, int r, int g, int f, bool ok) {
     const float sc = ok ? ws[f] : 0.0f;
     u32x4 x0[MT], x1[MT];
 #pragma unroll
@@ -201,7 +221,35 @@ __global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_kernel(GemvArgs a) {
       for (int m = 0; m < MT; ++m)
         if (m < M) part[m * RG + f] = p[m];
     }
-  });
+  };
+  const unsigned char *xsrc = reinterpret_cast<const unsigned char *>(a.x + (int64_t)rv.xrow * a.ldx);
+  // One batch, as in w8a8_gemv_kernel: activations and scales requested
+  // before the weights, staged in LDS after them.
+  constexpr int XN = 2 * MT;
+  if (rv.rvalid * G <= kGemvLoads * 8 * (kGemvThreads / 64) &&
+      M * K * 2 <= XN * 16 * kGemvThreads) {
+    RowStage<XN> cst;
+    cst.load(xsrc, a.ldx * 2, M, K * 2);
+    const int tw = min((int)threadIdx.x, rv.rvalid * G - 1);
+    const float wsv = rv.s[(int64_t)rv.map(tw / G) * G + tw % G];
+    RowLoads<kGemvLoads> L;
+    L.issue(rv.rvalid, G, row_ptr);
+    cst.store(reinterpret_cast<unsigned char *>(xl));
+    if ((int)threadIdx.x < rv.rvalid * G) ws[threadIdx.x] = wsv;
+    __syncthreads();
+    L.consume(body);
+  } else {
+    for (int i = threadIdx.x; i < M * K / 8; i += blockDim.x) {
+      const int m = (i * 8) / K, c = (i * 8) - m * K;
+      *reinterpret_cast<u32x4 *>(xl + m * K + c) = ldg16(a.x + (int64_t)(rv.xrow + m) * a.ldx + c);
+    }
+    for (int i = threadIdx.x; i < rv.rvalid * G; i += blockDim.x) {
+      const int r = i / G, g = i - r * G;
+      ws[i] = rv.s[(int64_t)rv.map(r) * G + g];
+    }
+    __syncthreads();
+    stream_rows<kGemvLoads>(rv.rvalid, G, row_ptr, body);
+  }
   __syncthreads();
 
   for (int i = threadIdx.x; i < M * rv.rvalid; i += blockDim.x) {

@@ -123,6 +123,98 @@ struct RowLoads {
   }
 };
 
+// Two-phase forms of the activation staging below, for kernels that issue
+// their weight loads in between: load() requests the activations, store()
+// writes them (quantized, for QuantStage) to LDS.  The memory counter
+// completes in issue order, so the wait before store() covers only these
+// older loads, not the weights.  Loads are branch-free (pieces or jobs past
+// the end re-read the last one); only the stores are guarded.
+// RowStage: `rows` rows of `row_bytes` bytes (a multiple of 16), at most N
+// 16-byte pieces per thread (rows * row_bytes <= N * 16 * blockDim.x).
+template <int N>
+struct RowStage {
+  u32x4 v[N];
+  int n;
+  __device__ __forceinline__ void load(const unsigned char *src, int64_t pitch, int rows,
+                                       int row_bytes) {
+    const int per_row = row_bytes >> 4;
+    n = rows * per_row;
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+      const int i = min((int)(threadIdx.x + u * blockDim.x), n - 1);
+      const int m = i / per_row, c = i - (i / per_row) * per_row;
+      v[u] = ldg16(src + m * pitch + c * 16);
+    }
+  }
+  __device__ __forceinline__ void store(unsigned char *dst) const {
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+      const int i = threadIdx.x + u * blockDim.x;
+      if (i < n) *reinterpret_cast<u32x4 *>(dst + (int64_t)i * 16) = v[u];
+    }
+  }
+};
+
+// Absmax of a 128-group held as 4 values per lane by one half-wave: four DPP
+// steps inside each 16-lane row, one shuffle across the half-wave's two rows.
+__device__ __forceinline__ float halfwave_max(float a) {
+  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0xB1, 0xF, 0xF, false)));
+  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x4E, 0xF, 0xF, false)));
+  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x141, 0xF, 0xF, false)));
+  a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x140, 0xF, 0xF, false)));
+  return fmaxf(a, __shfl_xor(a, 16, 64));
+}
+
+// Quantizes one 128-group (4 values per lane of a half-wave, w8a8.py:8-14)
+// into xq[g * 128 + 4 l ..] and, from lane 0, its scale; `store` guards both.
+template <typename T>
+__device__ __forceinline__ void quantize_group(uint2 raw, int l, bool store, int8_t *xq_group,
+                                               float *xs_slot) {
+  const float inv127 = (float)(1.0 / 127.0);
+  float v[4] = {T::to_f32(raw.x & 0xFFFFu), T::to_f32(raw.x >> 16), T::to_f32(raw.y & 0xFFFFu),
+                T::to_f32(raw.y >> 16)};
+  const float a =
+      halfwave_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  const float sc = fmaxf(a, 1e-10f) * inv127;
+  uint32_t packed = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[i] / sc)) << (8 * i);
+  if (store) {
+    *reinterpret_cast<uint32_t *>(xq_group + l * 4) = packed;
+    if (l == 0) *xs_slot = sc;
+  }
+}
+
+// QuantStage: a half-wave owns (row, group) jobs half, half + nhalf, ... (at
+// most J of them: rows * (K / 128) <= J * blockDim.x / 32).
+template <typename T, int J>
+struct QuantStage {
+  uint2 raw[J];
+  int jobs, G;
+  __device__ __forceinline__ void load(const uint16_t *x, int64_t ldx, int rows, int K) {
+    G = K >> 7;
+    jobs = rows * G;
+    const int half = threadIdx.x >> 5, nhalf = blockDim.x >> 5, l = threadIdx.x & 31;
+#pragma unroll
+    for (int u = 0; u < J; ++u) {
+      const int job = min(half + u * nhalf, jobs - 1);
+      const int m = job / G, g = job - (job / G) * G;
+      raw[u] = *reinterpret_cast<const uint2 *>(x + m * ldx + g * 128 + l * 4);
+    }
+  }
+  __device__ __forceinline__ void store(int K, int8_t *xq, float *xs) const {
+    const int half = threadIdx.x >> 5, nhalf = blockDim.x >> 5, l = threadIdx.x & 31;
+#pragma unroll
+    for (int u = 0; u < J; ++u) {
+      const int jr = half + u * nhalf;
+      const int job = min(jr, jobs - 1);
+      const int m = job / G, g = job - (job / G) * G;
+      quantize_group<T>(raw[u], l, jr < jobs, xq + m * K + g * 128, xs + m * G + g);
+    }
+  }
+};
+
 // Per-row dynamic quantization of `rows` activation rows of K 16-bit values
 // into LDS (w8a8.py:8-14).  Each 128-group is handled by 32 lanes.
 template <typename T>
@@ -132,7 +224,6 @@ __device__ __forceinline__ void quantize_rows_to_lds(const uint16_t *x, int64_t 
   const int half = threadIdx.x >> 5;
   const int nhalf = blockDim.x >> 5;
   const int l = threadIdx.x & 31;
-  const float inv127 = (float)(1.0 / 127.0);
   // Jobs (row m, group g) in batches of B per half-wave.  Every load of a
   // batch is issued before the first is used, and the jobs are computed
   // branch-free (jobs past the end redo the last one; only the stores are
@@ -154,23 +245,7 @@ __device__ __forceinline__ void quantize_rows_to_lds(const uint16_t *x, int64_t 
       const int jr = base + u * nhalf;
       const int job = min(jr, jobs - 1);
       const int m = job / G, g = job - (job / G) * G;
-      float v[4] = {T::to_f32(raw[u].x & 0xFFFFu), T::to_f32(raw[u].x >> 16),
-                    T::to_f32(raw[u].y & 0xFFFFu), T::to_f32(raw[u].y >> 16)};
-      float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-      a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0xB1, 0xF, 0xF, false)));
-      a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x4E, 0xF, 0xF, false)));
-      a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x141, 0xF, 0xF, false)));
-      a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x140, 0xF, 0xF, false)));
-      a = fmaxf(a, __shfl_xor(a, 16, 64));
-      const float sc = fmaxf(a, 1e-10f) * inv127;
-      uint32_t packed = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[i] / sc)) << (8 * i);
-      if (jr < jobs) {
-        *reinterpret_cast<uint32_t *>(xq + m * K + g * 128 + l * 4) = packed;
-        if (l == 0) xs[m * G + g] = sc;
-      }
+      quantize_group<T>(raw[u], l, jr < jobs, xq + m * K + g * 128, xs + m * G + g);
     }
   }
 }
