@@ -469,8 +469,13 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a, int
   const int tok = blockIdx.x;
   const int t = threadIdx.x;
   constexpr int PER = kH / 256;
-  if (tok < kE) {
-    const u32x4 wv = ldg16(a.router_w + (int64_t)tok * kH + t * PER);
+  // Both weight rows are requested at entry, ahead of the token's row, so
+  // their latency overlaps the RMSNorm; the router-row norm (blocks < E) is
+  // finished after the token's work, which it must not delay.
+  const u32x4 wv = tok < kE ? ldg16(a.router_w + (int64_t)tok * kH + t * PER)
+                            : u32x4{0u, 0u, 0u, 0u};
+  const u32x4 gv = ldg16(a.gate_w + t * PER);
+  auto router_row_norm = [&]() {
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -478,12 +483,15 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a, int
       ss += lo * lo + hi * hi;
     }
     ss = wave_sum_f32(ss);
+    __syncthreads();  // red2 is free again
     if ((t & 63) == 0) red2[t >> 6] = ss;
     __syncthreads();
     if (t == 0) a.nw[tok] = sqrtf((red2[0] + red2[1]) + (red2[2] + red2[3]));
-    __syncthreads();
+  };
+  if (tok >= T) {
+    if (tok < kE) router_row_norm();
+    return;
   }
-  if (tok >= T) return;
   norm_row_to_lds(a.h + (int64_t)tok * kH, a.norm_w, a.eps, xf, red);
   {
     float ss = 0.0f;
@@ -497,7 +505,6 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a, int
   for (int j = 0; j < 4; ++j)
     packed[j] = BF16::pack2(xf[t * PER + 2 * j], xf[t * PER + 2 * j + 1]);
   *reinterpret_cast<u32x4 *>(a.xn + (int64_t)tok * kH + t * PER) = packed;
-  const u32x4 gv = ldg16(a.gate_w + t * PER);
   double acc = 0.0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -511,6 +518,7 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a, int
     a.gl[tok] = round_bf16((float)(dred[0] + dred[1] + dred[2] + dred[3]));
     a.nx[tok] = sqrtf((red2[0] + red2[1]) + (red2[2] + red2[3]));
   }
+  if (tok < kE) router_row_norm();
 }
 
 // Approximate router logits of the prefill tokens: bf16 MFMA with fp32
