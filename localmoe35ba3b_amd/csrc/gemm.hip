@@ -61,8 +61,10 @@ __device__ __forceinline__ bool xcd_tile(const GemmArgs &a, int &mt, int &nt) {
   return mt < a.mt_count;
 }
 
-static unsigned xcd_grid(int mtiles, int ntiles) {
-  return (unsigned)(8 * ntiles * ((mtiles + 7) / 8));
+// Workgroups of an XCD-mapped launch; callers reject counts beyond one
+// launch's grid (2^31 - 1) before launching.
+static int64_t xcd_grid(int64_t mtiles, int64_t ntiles) {
+  return 8 * ntiles * ((mtiles + 7) / 8);
 }
 
 template <typename T, int BM, int WM, bool SWIGLU, bool GATHER, bool DENSE>
@@ -777,20 +779,22 @@ static int launch_grouped(GemmArgs a, unsigned mtiles, hipStream_t st) {
     constexpr int RBN = LM_RB_NW * LM_RB_TN;
     a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, RBN / 2) : (int)cdiv(a.N, RBN);
     a.mt_count = (int)mtiles;
-    const unsigned grid = xcd_grid(a.mt_count, a.nt_count);
+    const int64_t grid = xcd_grid(a.mt_count, a.nt_count);
+    LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
     if (a.K == 2048)
       grouped_rb_kernel<SWIGLU, GATHER, 2048, 96, LM_RB_TN, LM_RB_BD, LM_RB_HL, LM_RB_AD, LM_RB_NW,
-                        LM_RB_OCC><<<grid, LM_RB_NW * 64, 0, st>>>(a);
+                        LM_RB_OCC><<<(unsigned)grid, LM_RB_NW * 64, 0, st>>>(a);
     else
       grouped_rb_kernel<SWIGLU, GATHER, 512, 96, LM_RB_TN, LM_RB_BD, LM_RB_HL, LM_RB_AD, LM_RB_NW,
-                        LM_RB_OCC><<<grid, LM_RB_NW * 64, 0, st>>>(a);
+                        LM_RB_OCC><<<(unsigned)grid, LM_RB_NW * 64, 0, st>>>(a);
     return check_launch("grouped_rb_kernel");
   }
   constexpr int BN = LM_GROUPED_BN;
   a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, BN / 2) : (int)cdiv(a.N, BN);
   a.mt_count = (int)mtiles;
-  const unsigned grid = xcd_grid(a.mt_count, a.nt_count);
-  grouped_mfma_kernel<SWIGLU, GATHER, BN><<<grid, 256, 0, st>>>(a);
+  const int64_t grid = xcd_grid(a.mt_count, a.nt_count);
+    LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
+  grouped_mfma_kernel<SWIGLU, GATHER, BN><<<(unsigned)grid, 256, 0, st>>>(a);
   return check_launch("grouped_mfma_kernel");
 }
 
@@ -800,8 +804,9 @@ static int launch_gemm(GemmArgs a, unsigned mtiles, hipStream_t st) {
   a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, kBN / 2) : (int)cdiv(a.N, kBN);
   a.mt_count = (int)mtiles;
   if (mtiles == 0) return LM_OK;
-  w8a16_mfma_kernel<T, BM, WM, SWIGLU, GATHER, DENSE>
-      <<<xcd_grid(a.mt_count, a.nt_count), 256, 0, st>>>(a);
+  const int64_t grid = xcd_grid(a.mt_count, a.nt_count);
+  LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
+  w8a16_mfma_kernel<T, BM, WM, SWIGLU, GATHER, DENSE><<<(unsigned)grid, 256, 0, st>>>(a);
   return check_launch("w8a16_mfma_kernel");
 }
 

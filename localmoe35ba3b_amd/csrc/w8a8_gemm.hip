@@ -255,11 +255,12 @@ extern "C" int lm_w8a8_gemm(const int8_t *xq, const float *xs, const int8_t *q, 
   a.ldy = (int)(swiglu ? n / 2 : n);
   a.nt_count = (int)(swiglu ? cdiv(n / 2, kQBN / 2) : cdiv(n, kQBN));
   a.mt_count = (int)cdiv(m, kQBM);
-  const unsigned grid = (unsigned)(8 * a.nt_count * ((a.mt_count + 7) / 8));
+  const int64_t grid = 8 * (int64_t)a.nt_count * ((a.mt_count + 7) / 8);
+  LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
   hipStream_t st = as_stream(stream);
   if (swiglu)
-    w8a8_mfma_kernel<true, kQBN, kQOcc><<<grid, 256, 0, st>>>(a);
+    w8a8_mfma_kernel<true, kQBN, kQOcc><<<(unsigned)grid, 256, 0, st>>>(a);
   else
-    w8a8_mfma_kernel<false, kQBN, kQOcc><<<grid, 256, 0, st>>>(a);
+    w8a8_mfma_kernel<false, kQBN, kQOcc><<<(unsigned)grid, 256, 0, st>>>(a);
   return check_launch("w8a8_mfma_kernel");
 }

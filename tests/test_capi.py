@@ -57,6 +57,12 @@ def test_invalid_geometry_rejected_before_launch():
     assert lib.lm_w8a8_gemm(None, None, None, None, None, 9, 64, 128, 0, None) == _lib.LM_EINVAL
     assert b'null pointer' in lib.lm_last_error()
     assert lib.lm_w8a8_gemm(None, None, None, None, None, 0, 64, 128, 0, None) == _lib.LM_OK
+    # a grid beyond one launch is refused before anything is launched (the
+    # non-null placeholder pointers are never dereferenced)
+    fake = ctypes.c_void_p(256)
+    assert lib.lm_w8a8_gemm(fake, fake, fake, fake, fake, 1 << 24, 1 << 24, 128, 0,
+                            None) == _lib.LM_EINVAL
+    assert b'too large' in lib.lm_last_error()
 
 
 def test_status_maps_to_reference_exceptions():
