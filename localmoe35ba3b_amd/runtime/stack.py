@@ -167,6 +167,12 @@ class MoEStack:
         alone, so the result is bit-identical to overlap=False.  The schedule
         is stream-ordered and HIP-graph capturable.
         """
+        if h.dtype != torch.bfloat16 or not h.is_contiguous() or h.dim() != 2 or h.shape[-1] != self.H:
+            raise ValueError('expected contiguous bf16 [tokens, 2048] hidden states')
+        if chunk < 1:
+            raise ValueError('chunk must be positive')
+        if min(chunk, h.shape[0]) > self.max_tokens:  # before anything is queued
+            raise MemoryError('token count exceeds the workspace of this stack')
         starts = list(range(0, h.shape[0], chunk))
         if not overlap or len(starts) == 1:
             for c0 in starts:

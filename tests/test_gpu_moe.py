@@ -161,6 +161,19 @@ def test_overlapped_prefill(stack, dev, tokens, chunk):
         assert torch.equal(static, serial), f'replay {i}'
 
 
+def test_prefill_rejects_oversized_chunk(stack, dev):
+    """A chunk larger than the workspace is refused before any work is queued
+    (the hidden states stay untouched)."""
+    h = inputs(4096, 22, dev)
+    before = h.clone()
+    with pytest.raises(MemoryError):
+        stack.prefill_(h, chunk=4096)
+    with pytest.raises(ValueError):
+        stack.prefill_(h.float(), chunk=2048)
+    torch.cuda.synchronize()
+    assert torch.equal(h, before)
+
+
 def test_skewed_router_bias(dev):
     st = SyntheticMoEStack(layers=1, seed=12, device=dev, max_tokens=256,
                            router_bias=zipf_bias())
