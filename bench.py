@@ -314,8 +314,9 @@ def cpu_baseline(stack, x, dec_in, cores):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f'bench.py measures one GPU; --gpus {args.gpus} is not supported by this build '
-              '(the path would shard experts across GPUs, see DESIGN.md)', file=sys.stderr)
+        print(f'bench.py measures one GPU; --gpus {args.gpus} is not supported (across GPUs the '
+              'path would replicate the bank per GPU or shard experts with an all-to-all per '
+              'layer; neither is built)', file=sys.stderr)
         sys.exit(2)
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from localmoe35ba3b_amd.runtime.stack import SyntheticMoEStack

@@ -1,7 +1,8 @@
 """CPU oracle of the quantized MoE-FFN hot path - TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
-this module, and only as the checker (or the timed CPU baseline).  The product
+this module, and only as the reference results are compared with (or the timed
+CPU baseline).  The product
 path (localmoe35ba3b_amd) never calls it.
 
 Each function restates the arithmetic of the reference path it cites
