@@ -125,13 +125,9 @@ __device__ __forceinline__ float octet_sum_f32(float v) {
   return v;
 }
 
-// Full 64-lane reductions through shuffles (used off the hot loops).
+// Full 64-lane fp32 sum through an xor butterfly (32, 16, ..., 1): the fixed
+// order of the RMSNorm reductions, which the oracle restates.
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;

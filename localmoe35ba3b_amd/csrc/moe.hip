@@ -133,20 +133,6 @@ __device__ __forceinline__ void norm_row_to_lds(const uint16_t *h, const float *
   __syncthreads();
 }
 
-__device__ __forceinline__ double dot_lds_f64(const float *xf, const uint16_t *w, int lane) {
-  double acc = 0.0;
-#pragma unroll
-  for (int k0 = lane * 8; k0 < kH; k0 += 512) {
-    const u32x4 wv = ldg16(w + k0);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc = __builtin_fma((double)xf[k0 + 2 * j], (double)bf16_bits_to_f32(wv[j] & 0xFFFFu), acc);
-      acc = __builtin_fma((double)xf[k0 + 2 * j + 1], (double)bf16_bits_to_f32(wv[j] >> 16), acc);
-    }
-  }
-  return wave_sum_f64(acc);
-}
-
 // Router logits of the decode token: blocks 0..E/4-1 take one expert per
 // wave (the router row is loaded before the RMSNorm so its HBM latency
 // overlaps the norm); block E/4 computes the shared-expert gate logit.
@@ -203,7 +189,7 @@ __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
                             acc);
       }
     }
-    acc = wave_sum_f64(acc);
+    acc = wave_sum_f64_dpp(acc);
     if (lane == 0) {
       float l = round_bf16((float)acc);
       if (routed) {
@@ -511,7 +497,7 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a, int
     acc = __builtin_fma((double)xf[t * PER + 2 * j], (double)bf16_bits_to_f32(gv[j] & 0xFFFFu), acc);
     acc = __builtin_fma((double)xf[t * PER + 2 * j + 1], (double)bf16_bits_to_f32(gv[j] >> 16), acc);
   }
-  acc = wave_sum_f64(acc);
+  acc = wave_sum_f64_dpp(acc);
   if ((t & 63) == 0) dred[t >> 6] = acc;
   __syncthreads();
   if (t == 0) {

@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) void router_logits_gemv(const uint16_t *__rest
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
     if (m < T) {
-      const double s = wave_sum_f64(acc[m]);
+      const double s = wave_sum_f64_dpp(acc[m]);
       if (lane == 0) {
         float l = round_bf16((float)s);
         if (bias) l = l + bias[e];
