@@ -8,7 +8,7 @@
 //
 // One 128-element group is handled by 32 lanes holding 4 elements each, so a
 // wave quantizes two groups per iteration with fully coalesced 16-byte loads.
-#include "common.hpp"
+#include "gemv_core.hpp"
 
 namespace lm {
 
@@ -48,36 +48,40 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t *__restri
                                                         int8_t *__restrict__ q,
                                                         float *__restrict__ s,
                                                         int64_t ngroups) {
-  const int lane = threadIdx.x & 63;
-  const int l = lane & 31;
-  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) >> 6;
-  const float inv127 = (float)(1.0 / 127.0);
-  for (int64_t g2 = wave; g2 * 2 < ngroups; g2 += nwaves) {
-    const int64_t grp = g2 * 2 + (lane >> 5);
-    const bool valid = grp < ngroups;
-    uint2 raw = make_uint2(0, 0);
-    if (valid) raw = *reinterpret_cast<const uint2 *>(x + grp * 128 + l * 4);
-    float v[4] = {T::to_f32(raw.x & 0xFFFFu), T::to_f32(raw.x >> 16), T::to_f32(raw.y & 0xFFFFu),
-                  T::to_f32(raw.y >> 16)};
-    float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  // A half-wave quantizes B groups per pass: all B loads are issued before
+  // the first is used and the groups are computed branch-free (only the
+  // stores are guarded), so a pass costs one load latency.
+  constexpr int B = 4;
+  const int l = threadIdx.x & 31;
+  const int64_t half = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  const int64_t nhalf = ((int64_t)gridDim.x * blockDim.x) >> 5;
+  for (int64_t base = half; base < ngroups; base += nhalf * B) {
+    uint2 raw[B];
 #pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
-    const float sc = fmaxf(a, 1e-10f) * inv127;
-    uint32_t packed = 0;
+    for (int u = 0; u < B; ++u) {
+      const int64_t grp = min(base + u * nhalf, ngroups - 1);
+      raw[u] = *reinterpret_cast<const uint2 *>(x + grp * 128 + l * 4);
+    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[i] / sc)) << (8 * i);
-    if (valid) {
-      *reinterpret_cast<uint32_t *>(q + grp * 128 + l * 4) = packed;
-      if (l == 0) s[grp] = sc;
+    for (int u = 0; u < B; ++u) {
+      const int64_t gr = base + u * nhalf;
+      const int64_t grp = min(gr, ngroups - 1);
+      quantize_group<T>(raw[u], l, gr < ngroups, q + grp * 128, s + grp);
     }
   }
 }
 
+
 static unsigned quant_grid(int64_t ngroups) {
   int64_t waves = (ngroups + 1) / 2;
   int64_t blocks = (waves + 3) / 4;
+  if (blocks > 4096) blocks = 4096;
+  return (unsigned)(blocks < 1 ? 1 : blocks);
+}
+
+// act_quant_kernel: one half-wave per 4 groups (8 half-waves per block).
+static unsigned act_quant_grid(int64_t ngroups) {
+  int64_t blocks = (ngroups + 31) / 32;
   if (blocks > 4096) blocks = 4096;
   return (unsigned)(blocks < 1 ? 1 : blocks);
 }
@@ -107,8 +111,8 @@ extern "C" int lm_act_quant_g128(const void *x, int x_dtype, int8_t *q, float *s
   if (ngroups == 0) return LM_OK;
   const uint16_t *xp = static_cast<const uint16_t *>(x);
   if (x_dtype == LM_BF16)
-    act_quant_kernel<BF16><<<quant_grid(ngroups), 256, 0, as_stream(stream)>>>(xp, q, s, ngroups);
+    act_quant_kernel<BF16><<<act_quant_grid(ngroups), 256, 0, as_stream(stream)>>>(xp, q, s, ngroups);
   else
-    act_quant_kernel<FP16><<<quant_grid(ngroups), 256, 0, as_stream(stream)>>>(xp, q, s, ngroups);
+    act_quant_kernel<FP16><<<act_quant_grid(ngroups), 256, 0, as_stream(stream)>>>(xp, q, s, ngroups);
   return check_launch("act_quant_kernel");
 }
