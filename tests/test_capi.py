@@ -65,6 +65,34 @@ def test_invalid_geometry_rejected_before_launch():
     assert b'too large' in lib.lm_last_error()
 
 
+def test_moe_layer_bounds_rejected_before_launch():
+    """The fused layer accepts 1..65536 tokens of the 2048/512/256/top-8
+    geometry, with a workspace sized for the token count; every refusal
+    happens before a launch (the placeholder pointers are never used)."""
+    lib = _lib.lib()
+    fake = 256
+    layer = _lib.MoeLayer(*([fake] * 8), 0, 0, 0, 0)
+    ws = lib.lm_moe_workspace_bytes(65536, 2048, 512, 256, 8)
+    assert ws > lib.lm_moe_workspace_bytes(2048, 2048, 512, 256, 8) > 0
+    assert lib.lm_moe_workspace_bytes(0, 2048, 512, 256, 8) == -1
+    assert lib.lm_moe_workspace_bytes(16, 4096, 512, 256, 8) == -1
+
+    def fwd(tokens, ws_bytes, hidden=2048, lay=layer):
+        return lib.lm_moe_layer_forward(ctypes.byref(lay), fake, tokens, hidden, 512, 256, 8,
+                                        1e-6, fake, ws_bytes, None, None, None, None)
+
+    assert fwd(0, ws) == _lib.LM_EINVAL
+    assert b'invalid token count' in lib.lm_last_error()
+    assert fwd(65537, 1 << 62) == _lib.LM_EINVAL
+    assert fwd(16, ws, hidden=4096) == _lib.LM_EINVAL
+    assert b'hidden 2048' in lib.lm_last_error()
+    assert fwd(65536, ws - 1) == _lib.LM_ENOMEM
+    assert fwd(2, lib.lm_moe_workspace_bytes(1, 2048, 512, 256, 8)) == _lib.LM_ENOMEM
+    hole = _lib.MoeLayer(*([fake] * 5), None, fake, fake, 0, 0, 0, 0)
+    assert fwd(16, ws, lay=hole) == _lib.LM_EINVAL
+    assert b'null layer weight' in lib.lm_last_error()
+
+
 def test_status_maps_to_reference_exceptions():
     with pytest.raises(ValueError, match='Invalid INT8 group geometry'):
         _lib.call('lm_w8a16_linear', None, None, None, None, 1, 8, 100, 0, 0, None)

@@ -90,6 +90,27 @@ def test_token_independence(stack, dev):
     assert torch.equal(whole, parts)
 
 
+def test_prefill_max_tokens(dev):
+    """The largest token count one call accepts (65536 tokens, 524288 routes,
+    about 2048 rows per expert): one call equals 32 calls of 2048 tokens bit
+    for bit, and a sample of tokens matches the oracle (routing exact,
+    outputs within the bf16 tolerance)."""
+    st = SyntheticMoEStack(layers=1, seed=41, device=dev, max_tokens=65536)
+    h = inputs(65536, 40, dev)
+    whole, ids, _ = run_layer(st, h)
+    parts = torch.cat([run_layer(st, h[i:i + 2048].contiguous())[0]
+                       for i in range(0, 65536, 2048)])
+    assert torch.equal(whole, parts)
+    counts = np.bincount(ids.cpu().numpy().reshape(-1), minlength=256)
+    assert counts.sum() == 65536 * 8 and counts.max() > 2048
+    sample = np.random.default_rng(3).choice(65536, 12, replace=False)
+    sample[0] = 65535
+    sub_ids = ids.cpu().numpy()[sample]
+    ref, (_, _, ri) = oracle_layer(st, npf(h[sample]), 0, sub_ids)
+    assert np.array_equal(sub_ids, ri)
+    assert_close(npf(whole[sample]), ref, BF16_TOL, 'prefill 65536 sample')
+
+
 def test_decode_graph_replay(stack, dev):
     h0 = inputs(1, 9, dev)
     eager = h0.clone()
