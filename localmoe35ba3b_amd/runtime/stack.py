@@ -174,6 +174,8 @@ class MoEStack:
         if min(chunk, h.shape[0]) > self.max_tokens:  # before anything is queued
             raise MemoryError('token count exceeds the workspace of this stack')
         starts = list(range(0, h.shape[0], chunk))
+        if not starts:  # no tokens: nothing to queue, no second workspace
+            return h
         if not overlap or len(starts) == 1:
             for c0 in starts:
                 self.forward(h[c0:c0 + chunk])

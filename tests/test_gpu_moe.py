@@ -193,6 +193,7 @@ def test_prefill_rejects_oversized_chunk(stack, dev):
         stack.prefill_(h.float(), chunk=2048)
     torch.cuda.synchronize()
     assert torch.equal(h, before)
+    assert stack.prefill(h[:0]).shape == (0, 2048)  # an empty prompt queues nothing
 
 
 def test_skewed_router_bias(dev):
