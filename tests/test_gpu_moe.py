@@ -207,6 +207,14 @@ def test_skewed_router_bias(dev):
     ref, (_, _, ri) = O.moe_layer(npf(h), layer, k=8, eps=EPS)
     assert np.array_equal(ids.cpu().numpy(), ri)
     assert_close(npf(out), ref, BF16_TOL, 'skewed prefill layer')
+    for seed in (30, 31):  # the decode path adds the same bias
+        h1 = inputs(1, seed, dev)
+        out1, ids1, wts1 = run_layer(st, h1)
+        layer1 = st.layer_host(0, experts=np.unique(ids1.cpu().numpy()))
+        ref1, (_, rw1, ri1) = O.moe_layer(npf(h1), layer1, k=8, eps=EPS)
+        assert np.array_equal(ids1.cpu().numpy(), ri1)
+        assert np.abs(npf(wts1) - rw1).max() <= 2.0 ** -8
+        assert_close(npf(out1), ref1, BF16_TOL, 'skewed decode layer')
 
 
 def _bf16_up(v):
