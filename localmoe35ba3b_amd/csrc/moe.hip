@@ -510,60 +510,77 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a, int
 // Approximate router logits of the prefill tokens: bf16 MFMA with fp32
 // accumulation (neither rounded to bf16 nor biased).  A workgroup owns 32
 // tokens x 64 experts; its four waves each take one quarter of K for the
-// whole tile (2 x 4 MFMA tiles, so every 16-byte row piece loaded feeds two
-// or four MFMAs) and the quarters are summed through LDS at the end.  K is
-// streamed in 32-wide stages through a kRaD-deep register ring.  The
-// summation order does not matter: prefill_topk_count_kernel bounds the
-// error of any order.
-constexpr int kRaTok = 32, kRaExp = 64, kRaD = 4;
+// whole tile (2 x 4 MFMA tiles, so every fragment read feeds two or four
+// MFMAs) and the quarters are summed through LDS at the end.  K is streamed
+// in 128-wide segments with coalesced loads: a wave load covers 4 whole
+// 256-byte row segments, one row per quarter-wave (a load in the MFMA
+// operand layout would touch 16 rows 4 KB apart per quarter-wave and keep
+// the address path stalled).  The segments go through the wave's own LDS
+// region (pitch 272 B, so the 16 rows of a fragment read fall in distinct
+// banks) and are read back in the MFMA layout; the next segment's loads are
+// in flight meanwhile.  The summation order does not matter:
+// prefill_topk_count_kernel bounds the error of any order.
+constexpr int kRaTok = 32, kRaExp = 64;
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void
 router_approx_kernel(LayerArgs a, int T) {
   constexpr int KQ = kH / 4;
-  constexpr int NS = KQ / 32;
-  static_assert(NS % kRaD == 0 && kE % kRaExp == 0, "router tiling");
+  constexpr int SS = 128, NSS = KQ / SS, PITCH = 272;
+  constexpr int NLD = (kRaTok + kRaExp) / 4;  // wave loads per segment: 8 token + 16 expert
+  static_assert(KQ % SS == 0 && kE % kRaExp == 0 && kRaTok == 32 && kRaExp == 64, "router tiling");
   __shared__ f32x4 part[3][8][64];
+  __shared__ __align__(16) unsigned char stg[4][(kRaTok + kRaExp) * PITCH];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int q = lane >> 4, r = lane & 15;
   const int t0 = blockIdx.x * kRaTok;
   const int e0 = blockIdx.y * kRaExp;
-  const int kb = wave * KQ + q * 8;
-  const uint16_t *xa[2], *wb[4];
+  unsigned char *my = stg[wave];
+  // wave load j: staging rows 4 j .. 4 j + 3 (0..31 tokens, 32..95 experts),
+  // row 4 j + lane / 16, values 8 (lane % 16) .. + 7 of the segment
+  const int lr = lane >> 4, lc = lane & 15;
+  const uint16_t *src[NLD];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) xa[i] = a.xn + (int64_t)min(t0 + 16 * i + r, T - 1) * kH + kb;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) wb[j] = a.router_w + (int64_t)(e0 + 16 * j + r) * kH + kb;
+  for (int j = 0; j < NLD; ++j) {
+    src[j] = j < kRaTok / 4 ? a.xn + (int64_t)min(t0 + 4 * j + lr, T - 1) * kH
+                            : a.router_w + (int64_t)(e0 + 4 * (j - kRaTok / 4) + lr) * kH;
+    src[j] += wave * KQ + lc * 8;
+  }
   f32x4 acc[2][4];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  u32x4 ra[kRaD][2], rb[kRaD][4];
-  auto load = [&](int slot, int st) {
-    const int k = min(st, NS - 1) * 32;  // past the end the last stage is re-read, never used
+  u32x4 rg[NLD];
+  auto gload = [&](int ss) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) ra[slot][i] = ldg16(xa[i] + k);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) rb[slot][j] = ldg16(wb[j] + k);
+    for (int j = 0; j < NLD; ++j) rg[j] = ldg16(src[j] + ss * SS);
   };
+  gload(0);
+  for (int ss = 0; ss < NSS; ++ss) {
 #pragma unroll
-  for (int d = 0; d < kRaD; ++d) load(d, d);
-  for (int s0 = 0; s0 < NS; s0 += kRaD) {
+    for (int j = 0; j < NLD; ++j)
+      *reinterpret_cast<u32x4 *>(my + (4 * j + lr) * PITCH + lc * 16) = rg[j];
+    // the segment is read across lanes: every lane's stores come first
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (ss + 1 < NSS) gload(ss + 1);
 #pragma unroll
-    for (int u = 0; u < kRaD; ++u) {
+    for (int st = 0; st < SS / 32; ++st) {  // 32-wide MFMA steps: values 32 st + 8 q .. + 7
       u32x4 av[2], bv[4];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) av[i] = ra[u][i];
+      for (int i = 0; i < 2; ++i)
+        av[i] = *reinterpret_cast<const u32x4 *>(my + (16 * i + r) * PITCH + st * 64 + q * 16);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = rb[u][j];
-      load(u, s0 + u + kRaD);
+      for (int j = 0; j < 4; ++j)
+        bv[j] = *reinterpret_cast<const u32x4 *>(my + (kRaTok + 16 * j + r) * PITCH + st * 64 +
+                                                 q * 16);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = BF16::mfma16x16x32(av[i], bv[j], acc[i][j]);
-      // one stage per scheduling region: the refills stay kRaD stages ahead
-      __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_wave_barrier();  // every lane's reads before the next segment is stored
   }
   if (wave > 0) {
 #pragma unroll
