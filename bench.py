@@ -43,6 +43,8 @@ def parse():
     p.add_argument('--warmup', type=int, default=2)
     p.add_argument('--layers', type=int, default=40)
     p.add_argument('--no-cpu-baseline', action='store_true')
+    p.add_argument('--cpu-decode-tokens', type=int, default=DECODE_TOKENS,
+                   help='decode tokens the CPU baseline runs through all layers (default: all 33)')
     p.add_argument('--no-events', action='store_true',
                    help='time whole steps only (no per-phase HIP events)')
     p.add_argument('--copy-probe', action='store_true',
@@ -241,14 +243,17 @@ def skewed_prefill_probe(dev, reps=5):
     """One MoE layer on a 2048-token chunk with the router logits biased by a
     Zipf(1.1) per-expert offset (runtime.stack.zipf_bias): few hot experts
     with many rows each, many empty.  Times each phase with HIP events and
-    reports the grouped GEMMs against the bf16 MFMA peak."""
+    reports the grouped GEMMs against the bf16 MFMA peak.  Returns the
+    report and the layer's host copy, input and output (the CPU baseline
+    times the same layer)."""
     from localmoe35ba3b_amd.runtime.stack import SyntheticMoEStack, zipf_bias
     st = SyntheticMoEStack(layers=1, seed=3, device=dev, max_tokens=CHUNK, router_bias=zipf_bias())
     gen = torch.Generator(device=dev)
     gen.manual_seed(3)
     x = torch.randn((CHUNK, H), generator=gen, device=dev).to(torch.bfloat16)
     ids = torch.empty((CHUNK, K), dtype=torch.int32, device=dev)
-    st.layer_forward(x.clone(), 0, ids)
+    out = x.clone()
+    st.layer_forward(out, 0, ids)
     torch.cuda.synchronize()
     counts = np.bincount(ids.cpu().numpy().reshape(-1), minlength=E)
     active = int((counts > 0).sum())
@@ -260,54 +265,127 @@ def skewed_prefill_probe(dev, reps=5):
           for i, p in enumerate(PREFILL_PHASES)}
     fl = prefill_flops()
     pb = prefill_bytes(active)
-    out = {'active_experts': active, 'max_rows': int(counts.max()),
-           'layer_us': round(sum(ms.values()) * 1e3, 2)}
+    report = {'active_experts': active, 'max_rows': int(counts.max()),
+              'layer_us': round(sum(ms.values()) * 1e3, 2)}
     for p in ('gate_up', 'down'):
         us = ms[p] * 1e3
-        out[p] = {'avg_us': round(us, 2), 'tflops': round(fl[p] / us / 1e6, 1),
-                  'mfma_frac': round(fl[p] / us / 1e6 / BF16_PEAK_TFLOPS, 4),
-                  'bytes_per_launch': pb[p], 'gbs': round(pb[p] / us / 1e3, 1)}
+        report[p] = {'avg_us': round(us, 2), 'tflops': round(fl[p] / us / 1e6, 1),
+                     'mfma_frac': round(fl[p] / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                     'bytes_per_launch': pb[p], 'gbs': round(pb[p] / us / 1e3, 1)}
+    host = {'layer': st.layer_host(0), 'x': x.float().cpu().numpy(),
+            'out': out.float().cpu().numpy(), 'ids': ids.cpu().numpy()}
     del st
     torch.cuda.empty_cache()
-    return out
+    return report, host
 
 
-def cpu_baseline(stack, x, dec_in, cores):
-    """The CPU oracle (dequantize-then-matmul, the reference arithmetic on the
-    host) on a bounded sample: one 2048-token prefill chunk through one layer
-    and one decode token through every layer; extrapolated to tok/s."""
+def cpu_info():
+    """CPU model, logical CPUs this process may run on, and the physical cores
+    among them (distinct (package, core) pairs of the sysfs topology)."""
+    model = 'unknown'
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                model = line.split(':', 1)[1].strip()
+                break
+    except OSError:
+        pass
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        base = f'/sys/devices/system/cpu/cpu{c}/topology/'
+        try:
+            cores.add((open(base + 'physical_package_id').read().strip(),
+                       open(base + 'core_id').read().strip()))
+        except OSError:
+            cores.add(('?', str(c)))
+    return {'model': model, 'logical_cpus': len(cpus), 'physical_cores': len(cores)}
+
+
+def cpu_baseline(stack, x, decode_records, n_dec, zipf_host, threads, info):
+    """The CPU oracle (the reference's dequantize-then-matmul arithmetic on the
+    host: torch-CPU bf16 F.linear after dequantization, numpy int W8A8) timed
+    on this host with `threads` threads, on the workload's own inputs:
+      config 1  W8A16 [4096, 2048] at M = 1 and M = 2048, in full
+      config 2  W8A8 gate_up [1024, 2048] + SwiGLU at M = 1, 4, 8, in full
+      config 3  one MoE layer on one token (W8A8 routed experts): the mean of
+                the 40 x 33 token-layers of config 5's decode
+      config 4  one MoE layer on the Zipf-skewed 2048-token chunk, in full
+      config 5  decode: all 33 tokens through all 40 layers, in full, each
+                layer on the input the GPU saw there; prefill: one
+                2048-token chunk through one layer, extrapolated x80
+    The decode and Zipf runs assert what they compute: routing ids equal to
+    the GPU's bit for bit, layer outputs within the bf16 tolerance."""
     from oracle import moe_oracle as O
     from localmoe35ba3b_amd.runtime.stack import EPS
-    torch.set_num_threads(cores)
-    layer0 = stack.layer_host(0)
-    h = x[:CHUNK].float().cpu().numpy()
-    t0 = time.perf_counter()
-    O.moe_layer(h, layer0, k=K, eps=EPS)
-    t_chunk_layer = time.perf_counter() - t0
-    log(f'cpu prefill sample: {t_chunk_layer:.2f} s')
-    del layer0
-    # decode: one token through every layer.  Each layer gets the input the
-    # GPU saw at that layer, so routing (bit-exact) selects the same experts
-    # and only those are copied to the host beforehand.
-    ids_buf = torch.empty((1, K), dtype=torch.int32, device=x.device)
-    hg = dec_in[0].clone()
-    inputs, hosts, t_dec = [], [], 0.0
-    for l in range(stack.L):
-        inputs.append(hg.float().cpu().numpy())
-        stack.layer_forward(hg, l, ids_buf)
-        hosts.append(stack.layer_host(l, experts=ids_buf.cpu().numpy()[0]))
-    for l in range(stack.L):
+    torch.set_num_threads(threads)
+
+    def close(a, b, what):
+        rel = float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+        if not rel <= 2e-2:
+            raise AssertionError(f'cpu baseline: {what} differs from the GPU (rel {rel:.3e})')
+        return rel
+
+    out = {}
+    g = torch.Generator()
+    g.manual_seed(0)
+    wq, ws = O.quantize_weight((torch.randn(4096, H, generator=g) * 0.02).numpy())
+    for m in (1, 2048):
+        xm = O.bf16(torch.randn(m, H, generator=g).numpy())
         t0 = time.perf_counter()
-        O.moe_layer(inputs[l], hosts[l], k=K, eps=EPS)
-        t_dec += time.perf_counter() - t0
+        O.w8a16_linear(xm, wq, ws)
+        dt = time.perf_counter() - t0
+        out[f'w8a16_linear_m{m}'] = {'s': round(dt, 4), 'tok_s': round(m / dt, 2)}
+    gq, gs = O.quantize_weight((torch.randn(2 * I, H, generator=g) * 0.02).numpy())
+    for m in (1, 4, 8):
+        xm = O.bf16(torch.randn(m, H, generator=g).numpy())
+        t0 = time.perf_counter()
+        O.swiglu(O.w8a8_linear(xm, gq, gs))
+        dt = time.perf_counter() - t0
+        out[f'w8a8_gate_up_swiglu_m{m}'] = {'s': round(dt, 4), 'tok_s': round(m / dt, 2)}
+    log('cpu configs 1-2 done')
+    if zipf_host is not None:
+        t0 = time.perf_counter()
+        ref, (_, _, ri) = O.moe_layer(zipf_host['x'], zipf_host['layer'], k=K, eps=EPS)
+        dt = time.perf_counter() - t0
+        if not np.array_equal(ri, zipf_host['ids']):
+            raise AssertionError('cpu baseline: Zipf-chunk routing differs from the GPU')
+        rel = close(zipf_host['out'], ref, 'Zipf-chunk layer output')
+        out['zipf_prefill_layer'] = {'s': round(dt, 3), 'tok_s': round(CHUNK / dt, 2),
+                                     'rel_err_vs_gpu': round(rel, 6)}
+        log(f'cpu config 4 (Zipf chunk layer): {dt:.2f} s, routing exact')
+    layer0 = stack.layer_host(0)
+    t0 = time.perf_counter()
+    O.moe_layer(x[:CHUNK].float().cpu().numpy(), layer0, k=K, eps=EPS)
+    t_chunk_layer = time.perf_counter() - t0
+    del layer0
+    log(f'cpu prefill sample (one chunk, one layer): {t_chunk_layer:.2f} s')
+    t_dec, worst = 0.0, 0.0
+    for tok in range(n_dec):
+        for l, (h_in, ids, h_out, host) in enumerate(decode_records(tok)):
+            t0 = time.perf_counter()
+            ref, (_, _, ri) = O.moe_layer(h_in, host, k=K, eps=EPS)
+            t_dec += time.perf_counter() - t0
+            if not np.array_equal(ri, ids):
+                raise AssertionError(f'cpu baseline: decode token {tok} layer {l} routing differs')
+            worst = max(worst, close(h_out, ref, f'decode token {tok} layer {l} output'))
+        if tok % 8 == 7:
+            log(f'cpu decode: {tok + 1} tokens, {t_dec:.1f} s')
+    out['moe_layer_decode_1tok'] = {'s': round(t_dec / max(n_dec * stack.L, 1), 5)}
     prefill_tok_s = CHUNK / (t_chunk_layer * stack.L)
     return {
-        'value': round(prefill_tok_s, 3), 'unit': 'tok/s', 'cores': cores, 'kind': 'port',
-        'decode_tok_s': round(1.0 / t_dec, 4),
-        'sample': (f'oracle (torch-CPU dequant + F.linear, numpy W8A8) on {cores} threads: one '
+        'value': round(prefill_tok_s, 3), 'unit': 'tok/s', 'cores': threads, 'kind': 'port',
+        'decode_tok_s': round(n_dec / t_dec, 4) if n_dec else None,
+        'cpu': info, 'configs': out,
+        'checks': {'decode_token_layers': n_dec * stack.L, 'routing': 'bit-exact',
+                   'max_rel_err_vs_gpu': round(worst, 6)},
+        'sample': (f'oracle (torch-CPU dequant + F.linear, numpy int W8A8) on {threads} threads '
+                   f'of {info["physical_cores"]} physical cores ({info["model"]}): value = one '
                    f'2048-token prefill chunk through 1 of {stack.L} layers '
-                   f'({t_chunk_layer:.2f} s, prefill extrapolated x{stack.L}) and one decode '
-                   f'token through all {stack.L} layers ({t_dec:.2f} s)'),
+                   f'({t_chunk_layer:.2f} s), extrapolated x{stack.L} layers; decode = all '
+                   f'{n_dec} tokens through all {stack.L} layers in full ({t_dec:.1f} s) on the '
+                   f'GPU\'s per-layer inputs, routing asserted bit-exact and outputs within '
+                   f'2e-2; configs 1-4 timed in full'),
     }
 
 
@@ -501,11 +579,30 @@ def main():
                     'avg_us': k['avg_us']}
 
     kernels['lm_head_gemv'] = lm_head_probe(dev)  # after the timed steps, timed on its own
-    skewed = None if args.no_events else skewed_prefill_probe(dev)
+    skewed, zipf_host = (None, None) if args.no_events else skewed_prefill_probe(dev)
     isolated = None if args.no_events else isolated_probe(dev, 4 * spin_cycles)
 
-    cores = min(16, os.cpu_count() or 1)
-    cpu = None if args.no_cpu_baseline else cpu_baseline(stack, x, dec_in, cores)
+    cpu = None
+    if not args.no_cpu_baseline:
+        info = cpu_info()
+        threads = max(1, min(info['physical_cores'], 16))
+        ids_buf = torch.empty((1, K), dtype=torch.int32, device=dev)
+
+        def decode_records(i):
+            """Untimed: decode token i's per-layer inputs, routing and outputs
+            on the GPU, with host copies of the experts each layer selected."""
+            hg = dec_in[i].clone()
+            recs = []
+            for l in range(L):
+                h_in = hg.float().cpu().numpy()
+                stack.layer_forward(hg, l, ids_buf)
+                ids_np = ids_buf.cpu().numpy()
+                recs.append((h_in, ids_np, hg.float().cpu().numpy(),
+                             stack.layer_host(l, experts=ids_np[0])))
+            return recs
+
+        n_dec = min(args.cpu_decode_tokens, DECODE_TOKENS)
+        cpu = cpu_baseline(stack, x, decode_records, n_dec, zipf_host, threads, info)
 
     line = {
         'metric': 'MoE-FFN prefill/decode tok/s (4K chunk); decode HBM GB/s and % of peak',

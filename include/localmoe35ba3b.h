@@ -20,7 +20,14 @@
  *   weights  q int8 [N, K] row-major (K contiguous), K % 128 == 0
  *   scales   s fp32 [N, K/128]: w[n, k] ~= q[n, k] * s[n, k/128]
  *   expert banks are [E, N, K] / [E, N, K/128] with arbitrary expert stride.
- *   activations are bf16 (LM_BF16) or fp16 (LM_FP16) row-major.
+ *   activations are bf16 (LM_BF16) or fp16 (LM_FP16) row-major; a `dtype`
+ *   argument names the activation type, and outputs are written in it, as
+ *   the reference allocates its outputs in x.dtype.
+ *
+ * Indices that a kernel turns into addresses (expert ids, route positions,
+ * tile-table rows, combine slots) are clamped into the ranges the call
+ * states, so malformed routing data yields wrong values, never an access
+ * outside the buffers described by the arguments.
  *
  * Reference citations are to heliosz616/LocalMoe35Ba3b (qwen35_deploy/...)
  * and to the Transformers 5.15.0 Qwen3_5Moe modeling file ("HF").
@@ -69,26 +76,28 @@ int lm_w8a16_linear(const void *x, const int8_t *q, const float *s, void *y,
 
 /* Grouped W8A16 decode GEMV over a device descriptor table
  * table[e, 5] = {gate_up.q, gate_up.s, down.q, down.s, slot} (int64):
- * y[e, :] = x[shared ? 0 : e, :] . dequant(table[e, field..field+1])^T.
+ * y[e, :] = x[shared ? 0 : e, :] . dequant(table[e, field..field+1])^T,
+ * x and y of `dtype`.
  * Replaces int8.grouped_linear / int8._grouped_linear (int8.py:213-237). */
 int lm_w8a16_grouped_gemv(const void *x, const int64_t *table, void *y,
                           int64_t experts, int64_t n, int64_t k, int field,
-                          int shared, void *stream);
+                          int shared, int dtype, void *stream);
 
 /* Grouped W8A8 decode GEMV on pre-quantized activations (xq int8 [rows, k],
  * xs fp32 [rows, k/128]): int32 dot per 128-group, then
- * acc = acc + (float(p_g) * xs_g) * ws[n, g] in ascending g, no FMA.
+ * acc = acc + (float(p_g) * xs_g) * ws[n, g] in ascending g, no FMA;
+ * y written in y_dtype.
  * Replaces w8a8._linear (w8a8.py:25-41). */
 int lm_w8a8_grouped_gemv(const int8_t *xq, const float *xs,
                          const int64_t *table, void *y, int64_t experts,
                          int64_t n, int64_t k, int field, int shared,
-                         void *stream);
+                         int y_dtype, void *stream);
 
-/* lm_act_quant_g128 fused into lm_w8a8_grouped_gemv (x bf16).
+/* lm_act_quant_g128 fused into lm_w8a8_grouped_gemv; x and y of `dtype`.
  * Replaces w8a8.grouped_linear (w8a8.py:44-48). */
 int lm_w8a8_grouped_linear(const void *x, const int64_t *table, void *y,
                            int64_t experts, int64_t n, int64_t k, int field,
-                           int shared, void *stream);
+                           int shared, int dtype, void *stream);
 
 /* Exact int32 per-group partials p[m, n, g] = sum_{k in g} xq[m, k] * wq[n, k]
  * of the W8A8 GEMV inner product (the tl.dot of w8a8.py:37), computed by the
@@ -96,46 +105,50 @@ int lm_w8a8_grouped_linear(const void *x, const int64_t *table, void *y,
 int lm_w8a8_group_partials(const int8_t *xq, const int8_t *wq, int32_t *p,
                            int64_t m, int64_t n, int64_t k, void *stream);
 
-/* Dense W8A8 decode linear for m <= 8 rows of bf16 x: per-row dynamic
- * quantization, int32 group dots, the w8a8.py:40 fp32 epilogue, bf16 out.
+/* Dense W8A8 decode linear for m <= 8 rows of x (`dtype`): per-row dynamic
+ * quantization, int32 group dots, the w8a8.py:40 fp32 epilogue, y in dtype.
  * swiglu != 0 treats the n weight rows as [gate; up] halves and writes
- * y[m, n/2] = bf16(bf16(silu(gate)) * up) (HF:715, int8.py:182-184).
+ * y[m, n/2] = T(T(silu(gate)) * up) (HF:715, int8.py:182-184).
  * No reference counterpart as one call: it is w8a8.quantize + w8a8._linear
  * + the SwiGLU glue on one dense matrix. */
 int lm_w8a8_linear(const void *x, const int8_t *q, const float *s, void *y,
-                   int64_t m, int64_t n, int64_t k, int swiglu, void *stream);
+                   int64_t m, int64_t n, int64_t k, int swiglu, int dtype,
+                   void *stream);
 
 /* W8A8 MFMA GEMM for any number of rows (int8 x int8 -> int32 MFMA with
  * the per-group fp32 rescale), on rows already quantized by
  * lm_act_quant_g128: xq int8 [m, k], xs fp32 [m, k/128]; weights q int8
- * [n, k], s fp32 [n, k/128]; y bf16 [m, n], or [m, n/2] with swiglu as in
- * lm_w8a8_linear.  Replaces w8a8._linear (w8a8.py:25-41) applied to every
- * row rather than row 0 only: exact int32 group partials, then
+ * [n, k], s fp32 [n, k/128]; y [m, n] in y_dtype (bf16 or fp16), or
+ * [m, n/2] with swiglu as in lm_w8a8_linear.  Replaces w8a8._linear
+ * (w8a8.py:25-41) applied to every row rather than row 0 only: exact int32 group partials, then
  * acc = acc + (f32(p) * xs) * ws in ascending group order, unfused, so the
  * output is bit-identical to the reference's for each row. */
 int lm_w8a8_gemm(const int8_t *xq, const float *xs, const int8_t *q, const float *s,
-                 void *y, int64_t m, int64_t n, int64_t k, int swiglu, void *stream);
+                 void *y, int64_t m, int64_t n, int64_t k, int swiglu, int y_dtype,
+                 void *stream);
 
-/* bf16 SwiGLU glue: h[r, c] = bf16(bf16(silu(gu[r, c])) * gu[r, half + c]).
+/* SwiGLU glue in `dtype` T: h[r, c] = T(T(silu(gu[r, c])) * gu[r, half + c]).
  * Replaces `gate, up = gu.chunk(2, -1); silu(gate) * up`
  * (int8.py:182-184, prefill.py:77-78, gpu_routes.py:74-75). */
-int lm_swiglu(const void *gu, void *h, int64_t rows, int64_t half,
+int lm_swiglu(const void *gu, void *h, int64_t rows, int64_t half, int dtype,
               void *stream);
 
 /* Decode combine over the descriptor table, ascending table order:
- * acc = bf16(acc + bf16(v[e, c] * w[slot_e])).  w_dtype LM_BF16 or LM_FP32.
+ * acc = T(acc + T(v[e, c] * w[slot_e])), v and y of `dtype` T; w_dtype
+ * LM_BF16, LM_FP16 or LM_FP32; slots clamped into [0, experts).
  * Replaces int8._ordered_reduce (int8.py:240-250). */
 int lm_ordered_reduce(const void *v, const int64_t *table, const void *w,
                       int w_dtype, void *y, int64_t n, int64_t experts,
-                      void *stream);
+                      int dtype, void *stream);
 
 /* Prefill combine: per token over its top_k routes in ascending expert order
- * acc = bf16(acc + bf16(v[ordered[t,i], c] * w[t, slots[t,i]])).
+ * acc = T(acc + T(v[ordered[t,i], c] * w[t, slots[t,i]])), v and y of
+ * `dtype` T; routes clamped into [0, tokens * top_k), slots into [0, top_k).
  * Replaces prefill._reduce (prefill.py:37-49). */
 int lm_routed_reduce(const void *v, const int64_t *ordered,
                      const int64_t *slots, const void *w, int w_dtype,
                      void *y, int64_t tokens, int64_t n, int64_t top_k,
-                     void *stream);
+                     int dtype, void *stream);
 
 /* Device route plan of gpu_routes.plan + _table (gpu_routes.py:17-36,47-63):
  * stable sort of the flat ids by expert; pos[p] = token of the p-th sorted
@@ -159,27 +172,47 @@ int lm_plan_routes_host(const int64_t *ids, int64_t tokens, int64_t top_k,
                         int64_t *seg_expert, int64_t *seg_start,
                         int64_t *seg_stop, int64_t *n_segments);
 
+/* Host (CPU) twin of lm_route_plan for ids already on the host, the plan of
+ * the reference's host-planned prefill (prefill.py:52-85): pos[R] = token of
+ * the p-th route in stable expert order; table rows (expert, start, stop)
+ * for the bm-row tiles of the non-empty experts only (*n_tiles of them, in
+ * expert order; max_tiles >= cdiv(R, bm) + experts is the capacity);
+ * ordered/slots as in lm_route_plan; *n_active = number of non-empty
+ * experts.  Returns LM_EINVAL for an empty input or an out-of-range id. */
+int lm_route_plan_host(const int64_t *ids, int64_t tokens, int64_t top_k,
+                       int64_t experts, int64_t bm, int64_t *pos,
+                       int64_t *table, int64_t max_tiles, int64_t *ordered,
+                       int64_t *slots, int64_t *n_tiles, int64_t *n_active);
+
 /* Routed grouped W8A16 GEMM over a tile table (MFMA): for each tile
  * (e, start, stop) rows r in [start, min(start+bm, stop)):
  * y[r, :] = x[gather ? pos[r] : r, :] . dequant(q[e], s[e])^T.
- * bm must equal the table's tile height (<= 128).  Strides are in elements.
+ * x [x_rows, k] and y [y_rows, n] of `dtype`; the bank holds `experts`
+ * experts at the given strides (elements).  Table experts are clamped into
+ * [0, experts), starts and stops into [0, y_rows] and gathered rows pos[r]
+ * into [0, x_rows); without gather y_rows <= x_rows.  pos (gather) has
+ * y_rows entries.  bm must equal the table's tile height (<= 128).
  * Replaces prefill._routed / gpu_routes._nonempty (prefill.py:12-34,
  * gpu_routes.py:39-44). */
-int lm_routed_gemm_w8a16(const void *x, const int8_t *q, const float *s,
+int lm_routed_gemm_w8a16(const void *x, int64_t x_rows, const int8_t *q,
+                         const float *s, int64_t experts,
+                         int64_t q_expert_stride, int64_t s_expert_stride,
                          const int64_t *pos, const int64_t *table,
-                         int64_t n_tiles, int64_t bm, void *y, int64_t n,
-                         int64_t k, int gather, int64_t q_expert_stride,
-                         int64_t s_expert_stride, void *stream);
+                         int64_t n_tiles, int64_t bm, void *y, int64_t y_rows,
+                         int64_t n, int64_t k, int gather, int dtype,
+                         void *stream);
 
-/* lm_routed_gemm_w8a16 on the gate_up bank with the SwiGLU glue fused into
- * the epilogue: h[r, c] = bf16(bf16(silu(gu[r, c])) * gu[r, n/2 + c]),
- * h is [rows, n/2].  Same result as prefill.py:75-78 without the [R, n]
+/* lm_routed_gemm_w8a16 (gathered) on the gate_up bank with the SwiGLU glue
+ * fused into the epilogue: h[r, c] = T(T(silu(gu[r, c])) * gu[r, n/2 + c]),
+ * h is [h_rows, n/2].  Same result as prefill.py:75-78 without the [R, n]
  * intermediate. */
-int lm_routed_gate_up_swiglu(const void *x, const int8_t *q, const float *s,
+int lm_routed_gate_up_swiglu(const void *x, int64_t x_rows, const int8_t *q,
+                             const float *s, int64_t experts,
+                             int64_t q_expert_stride, int64_t s_expert_stride,
                              const int64_t *pos, const int64_t *table,
-                             int64_t n_tiles, int64_t bm, void *h, int64_t n,
-                             int64_t k, int64_t q_expert_stride,
-                             int64_t s_expert_stride, void *stream);
+                             int64_t n_tiles, int64_t bm, void *h,
+                             int64_t h_rows, int64_t n, int64_t k, int dtype,
+                             void *stream);
 
 /* HF Qwen3_5MoeTopKRouter (HF:768-776) with a fixed tie rule:
  * logits[t, e] = float(bf16(float(sum_k double(x[t,k]) * double(w[e,k]))))
@@ -212,10 +245,11 @@ int lm_rmsnorm(const void *x, const float *w, void *y, int64_t rows,
  * Decode (tokens == 1) runs routed experts W8A8 (w8a8.py) and the shared
  * expert W8A16; prefill runs everything W8A16 (prefill.py / gpu_routes.py).
  * H = 2048, I = 512, E = 256, top_k = 8 are the supported geometry.
- * `workspace` is caller-owned device memory of lm_moe_workspace_bytes();
- * it must start zeroed once (lm_moe_workspace_init) and is reused by every
- * later call on the same stream.  Calls sharing a workspace must not
- * overlap. */
+ * `workspace` is caller-owned device memory of lm_moe_workspace_bytes(),
+ * reused by every later call on the same stream; every call writes each
+ * workspace region before reading it, so its initial contents do not
+ * matter (lm_moe_workspace_init zeroes all of it for callers that want a
+ * defined state).  Calls sharing a workspace must not overlap. */
 typedef struct lm_moe_layer {
   const void *router_w;
   const float *router_bias;
@@ -234,6 +268,28 @@ typedef struct lm_moe_layer {
 int64_t lm_moe_workspace_bytes(int64_t max_tokens, int64_t hidden,
                                int64_t inter, int64_t experts, int64_t top_k);
 int lm_moe_workspace_init(void *workspace, int64_t bytes, void *stream);
+
+/* Where a prefill call (tokens > 1) on `tokens` rows leaves its
+ * intermediates in the workspace: byte offset and size of one region, for
+ * tests and debugging (no reference counterpart; the reference keeps these
+ * in separate torch tensors, prefill.py:52-85).  Regions:
+ *   LM_WS_NORMED      bf16  [tokens, H]      RMSNorm output (router input)
+ *   LM_WS_GATE        fp32  [tokens]         shared-expert gate logits
+ *   LM_WS_IDS         int64 [tokens, top_k]  selected experts, selection order
+ *   LM_WS_WEIGHTS     bf16  [tokens, top_k]  routing weights, same order
+ *   LM_WS_ROUTE_ROWS  int32 [tokens, top_k]  expert-sorted row of each route
+ *   LM_WS_HIDDEN      bf16  [R + tokens, I]  SwiGLU rows (routed, then shared)
+ *   LM_WS_DOWN        bf16  [R + tokens, H]  down rows (routed, then shared)
+ * with R = tokens * top_k.  Valid until the next call using the workspace. */
+#define LM_WS_NORMED 0
+#define LM_WS_GATE 1
+#define LM_WS_IDS 2
+#define LM_WS_WEIGHTS 3
+#define LM_WS_ROUTE_ROWS 4
+#define LM_WS_HIDDEN 5
+#define LM_WS_DOWN 6
+int lm_moe_workspace_region(int64_t tokens, int region, int64_t *offset,
+                            int64_t *bytes);
 
 /* One MoE-FFN layer on `tokens` rows of h (decode path when tokens == 1).
  * If ids_out / weights_out are non-NULL the routing of this layer is copied

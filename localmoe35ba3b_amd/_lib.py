@@ -14,6 +14,9 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / 'liblocalmoe35ba3b.so'
 
 LM_OK, LM_EINVAL, LM_ENOMEM, LM_ELAUNCH = 0, 1, 2, 3
 LM_BF16, LM_FP16, LM_FP32 = 0, 1, 2
+# fused-layer workspace regions (lm_moe_workspace_region)
+WS_REGIONS = {'normed': 0, 'gate': 1, 'ids': 2, 'weights': 3, 'route_rows': 4, 'hidden': 5,
+              'down': 6}
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64
@@ -27,23 +30,27 @@ SIGNATURES = {
     'lm_quantize_weight_g128': (I32, [P, P, P, I64, I64, P]),
     'lm_act_quant_g128': (I32, [P, I32, P, P, I64, I64, P]),
     'lm_w8a16_linear': (I32, [P, P, P, P, I64, I64, I64, I32, I32, P]),
-    'lm_w8a16_grouped_gemv': (I32, [P, P, P, I64, I64, I64, I32, I32, P]),
-    'lm_w8a8_grouped_gemv': (I32, [P, P, P, P, I64, I64, I64, I32, I32, P]),
-    'lm_w8a8_grouped_linear': (I32, [P, P, P, I64, I64, I64, I32, I32, P]),
+    'lm_w8a16_grouped_gemv': (I32, [P, P, P, I64, I64, I64, I32, I32, I32, P]),
+    'lm_w8a8_grouped_gemv': (I32, [P, P, P, P, I64, I64, I64, I32, I32, I32, P]),
+    'lm_w8a8_grouped_linear': (I32, [P, P, P, I64, I64, I64, I32, I32, I32, P]),
     'lm_w8a8_group_partials': (I32, [P, P, P, I64, I64, I64, P]),
-    'lm_w8a8_linear': (I32, [P, P, P, P, I64, I64, I64, I32, P]),
-    'lm_w8a8_gemm': (I32, [P, P, P, P, P, I64, I64, I64, I32, P]),
-    'lm_swiglu': (I32, [P, P, I64, I64, P]),
-    'lm_ordered_reduce': (I32, [P, P, P, I32, P, I64, I64, P]),
-    'lm_routed_reduce': (I32, [P, P, P, P, I32, P, I64, I64, I64, P]),
+    'lm_w8a8_linear': (I32, [P, P, P, P, I64, I64, I64, I32, I32, P]),
+    'lm_w8a8_gemm': (I32, [P, P, P, P, P, I64, I64, I64, I32, I32, P]),
+    'lm_swiglu': (I32, [P, P, I64, I64, I32, P]),
+    'lm_ordered_reduce': (I32, [P, P, P, I32, P, I64, I64, I32, P]),
+    'lm_routed_reduce': (I32, [P, P, P, P, I32, P, I64, I64, I64, I32, P]),
     'lm_route_plan': (I32, [P, I64, I64, I64, I64, P, P, I64, P, P, P]),
     'lm_plan_routes_host': (I32, [P, I64, I64, I64, P, P, P, P, P]),
-    'lm_routed_gemm_w8a16': (I32, [P, P, P, P, P, I64, I64, P, I64, I64, I32, I64, I64, P]),
-    'lm_routed_gate_up_swiglu': (I32, [P, P, P, P, P, I64, I64, P, I64, I64, I64, I64, P]),
+    'lm_route_plan_host': (I32, [P, I64, I64, I64, I64, P, P, I64, P, P, P, P]),
+    'lm_routed_gemm_w8a16': (I32, [P, I64, P, P, I64, I64, I64, P, P, I64, I64, P, I64, I64,
+                                   I64, I32, I32, P]),
+    'lm_routed_gate_up_swiglu': (I32, [P, I64, P, P, I64, I64, I64, P, P, I64, I64, P, I64,
+                                       I64, I64, I32, P]),
     'lm_router_topk': (I32, [P, P, P, P, P, P, I64, I64, I64, I64, P]),
     'lm_rmsnorm': (I32, [P, P, P, I64, I64, F32, P]),
     'lm_moe_workspace_bytes': (I64, [I64, I64, I64, I64, I64]),
     'lm_moe_workspace_init': (I32, [P, I64, P]),
+    'lm_moe_workspace_region': (I32, [I64, I32, P, P]),
     'lm_moe_layer_forward': (I32, [P, P, I64, I64, I64, I64, I64, F32, P, I64, P, P, P, P]),
 }
 

@@ -7,6 +7,7 @@
 #include <stdint.h>
 #include <string>
 
+#include "bounds.hpp"
 #include "localmoe35ba3b.h"
 
 namespace lm {
@@ -164,6 +165,19 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
   return v;
 }
 
+// ------------------------------------------------------------ wave LDS hand-off
+// Lanes of one wave handing data to each other through LDS: every LDS access
+// of the wave before this point is ordered before every LDS access after it.
+// The wave barrier alone is a scheduling barrier without memory semantics
+// (the compiler may move LDS accesses across it when it can prove them
+// disjoint); the wavefront-scope fences make the ordering a memory-model
+// guarantee.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ------------------------------------------------------------ loads
 __device__ __forceinline__ u32x4 ldg16(const void *p) {
   return *reinterpret_cast<const u32x4 *>(p);
@@ -220,16 +234,9 @@ __device__ __forceinline__ T row_max_keys(T k) {
 
 struct Key64 {
   using T = unsigned long long;
-  static __device__ __forceinline__ T make(float v, int idx) {
-    uint32_t b = __float_as_uint(v + 0.0f);
-    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return ((T)b << 32) | (uint32_t)(0xFFFFu - (uint32_t)idx);
-  }
-  static __device__ __forceinline__ int index(T k) { return (int)(0xFFFFu - (uint32_t)(k & 0xFFFFu)); }
-  static __device__ __forceinline__ float value(T k) {
-    const uint32_t b = (uint32_t)(k >> 32);
-    return __uint_as_float((b & 0x80000000u) ? (b & 0x7FFFFFFFu) : ~b);
-  }
+  static __device__ __forceinline__ T make(float v, int idx) { return key64_make(v, idx); }
+  static __device__ __forceinline__ int index(T k) { return key64_index(k); }
+  static __device__ __forceinline__ float value(T k) { return key64_value(k); }
   static __device__ __forceinline__ T row_max(T k) {
     return row_max_keys<T, dpp_u64<0xB1>, dpp_u64<0x4E>, dpp_u64<0x141>, dpp_u64<0x140>>(k);
   }
@@ -242,16 +249,9 @@ struct Key64 {
 
 struct Key32 {
   using T = uint32_t;
-  static __device__ __forceinline__ T make(float v, int idx) {
-    uint32_t b = __float_as_uint(v + 0.0f) >> 16;
-    b = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
-    return (b << 16) | (0xFFFFu - (uint32_t)idx);
-  }
-  static __device__ __forceinline__ int index(T k) { return (int)(0xFFFFu - (k & 0xFFFFu)); }
-  static __device__ __forceinline__ float value(T k) {
-    const uint32_t b = k >> 16;
-    return __uint_as_float(((b & 0x8000u) ? (b & 0x7FFFu) : (~b & 0xFFFFu)) << 16);
-  }
+  static __device__ __forceinline__ T make(float v, int idx) { return key32_make(v, idx); }
+  static __device__ __forceinline__ int index(T k) { return key32_index(k); }
+  static __device__ __forceinline__ float value(T k) { return key32_value(k); }
   static __device__ __forceinline__ T row_max(T k) {
     return row_max_keys<T, dpp_u32<0xB1>, dpp_u32<0x4E>, dpp_u32<0x141>, dpp_u32<0x140>>(k);
   }
@@ -341,13 +341,13 @@ __device__ __forceinline__ typename KT::T kth_key_wave(typename KT::T key[4], in
   using T = typename KT::T;
   T *scratch = reinterpret_cast<T *>(scratch_words);
   topk_row_winners<KT>(key, K, lane, scratch);
-  __builtin_amdgcn_wave_barrier();
+  wave_lds_sync();
   T mine;
   const int rank = topk_winner_rank<KT>(scratch, K, lane, mine);
-  __builtin_amdgcn_wave_barrier();
+  wave_lds_sync();
   T *out = reinterpret_cast<T *>(scratch_words + 64);
   if (lane < 4 * K && rank == K - 1) out[0] = mine;
-  __builtin_amdgcn_wave_barrier();
+  wave_lds_sync();
   return out[0];
 }
 
@@ -379,7 +379,7 @@ __device__ __forceinline__ void topk_wave_keys(const float v[4], int E, int K, i
                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16))) +
                       (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 32)) +
                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 48)));
-  __builtin_amdgcn_wave_barrier();
+  wave_lds_sync();
   // Rank of each row winner among all 4 K of them.
   const int nc = 4 * K;
   T mine;
@@ -388,7 +388,7 @@ __device__ __forceinline__ void topk_wave_keys(const float v[4], int E, int K, i
   const bool chosen = lane < nc && rank < K;
   const float pe = expf(KT::value(mine) - mx) / denom;
   if (chosen) prob[rank] = pe;
-  __builtin_amdgcn_wave_barrier();
+  wave_lds_sync();
   float psum = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i)

@@ -35,6 +35,11 @@ struct GemmArgs {
   const int64_t *pos;    // gather map (routed gate_up)
   const int64_t *table;  // [tiles, 3] (expert, start, stop)
   int64_t M;             // dense rows
+  // bounds of the routed mode: table experts are clamped into [0, experts),
+  // starts and stops into [0, y_rows], gathered row indices into [0, x_rows)
+  int64_t experts;
+  int64_t y_rows;
+  int64_t x_rows;
   const int8_t *q;
   int64_t q_es;
   const float *s;
@@ -86,17 +91,19 @@ __global__ __launch_bounds__(256) void w8a16_mfma_kernel(GemmArgs a) {
   int mt, nt;
   if (!xcd_tile(a, mt, nt)) return;
 
-  int64_t e = 0, start, stop;
+  int64_t e = 0, start;
+  int rows;
   if constexpr (DENSE) {
     start = (int64_t)mt * BM;
-    stop = a.M;
+    rows = (int)min((int64_t)BM, a.M - start);
   } else {
-    e = a.table[mt * 3];
-    start = a.table[mt * 3 + 1];
-    stop = a.table[mt * 3 + 2];
-    if (start >= stop) return;
+    const TileBounds tb = tile_bounds(a.table[mt * 3], a.table[mt * 3 + 1], a.table[mt * 3 + 2],
+                                      a.experts, a.y_rows, a.tile_rows);
+    if (tb.rows <= 0) return;
+    e = tb.expert;
+    start = tb.start;
+    rows = tb.rows;
   }
-  const int rows = (int)min((int64_t)(DENSE ? BM : a.tile_rows), stop - start);
   const int8_t *wq = a.q + e * a.q_es;
   const float *wsc = a.s + e * a.s_es;
   const int K = a.K;
@@ -122,7 +129,7 @@ __global__ __launch_bounds__(256) void w8a16_mfma_kernel(GemmArgs a) {
   for (int i = 0; i < ACH; ++i) {
     const int c = tid + 256 * i;
     const int r = min(c >> 3, rows - 1);
-    const int64_t xr = GATHER ? a.pos[start + r] : start + r;
+    const int64_t xr = GATHER ? clamp_index(a.pos[start + r], a.x_rows) : start + r;
     asrc[i] = a.x + xr * a.ldx + (c & 7) * 8;
   }
   const int8_t *bsrc[2];
@@ -245,19 +252,20 @@ __global__ __launch_bounds__(256) void w8a16_mfma_kernel(GemmArgs a) {
 constexpr int kGBM = 128;
 constexpr int kLDB = kBK + 8;  // int8 bytes per LDS row of the weight tile
 
-// Eight int8 weights -> eight bf16(q * s): the signed byte converts exactly
+// Eight int8 weights -> eight T(q * s): the signed byte converts exactly
 // (v_cvt_f32_i32 with a sign-extended byte operand), so q * s is the
-// correctly rounded fp32 product, then RNE to bf16 - bit-identical to
-// dequant8_bf16 with one operation fewer per four weights.
-__device__ __forceinline__ u32x4 dequant8s_bf16(uint2 w, float s) {
+// correctly rounded fp32 product, then RNE to T - bit-identical to
+// dequant8 with one operation fewer per four weights.
+template <typename T>
+__device__ __forceinline__ u32x4 dequant8s(uint2 w, float s) {
   float f[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     f[i] = (float)(int8_t)(w.x >> (8 * i)) * s;
     f[4 + i] = (float)(int8_t)(w.y >> (8 * i)) * s;
   }
-  return u32x4{BF16::pack2(f[0], f[1]), BF16::pack2(f[2], f[3]), BF16::pack2(f[4], f[5]),
-               BF16::pack2(f[6], f[7])};
+  return u32x4{T::pack2(f[0], f[1]), T::pack2(f[2], f[3]), T::pack2(f[4], f[5]),
+               T::pack2(f[6], f[7])};
 }
 
 // SiLU for the prefill epilogue from the hardware exp2 and reciprocal
@@ -266,16 +274,17 @@ __device__ __forceinline__ float silu_fast(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
 }
 
-__device__ __forceinline__ u32x4 dequant8_bf16(uint2 w, float s) {
+template <typename T>
+__device__ __forceinline__ u32x4 dequant8(uint2 w, float s) {
   const float n = -128.0f * s;
   float f[8];
   dequant4(w.x, s, n, f);
   dequant4(w.y, s, n, f + 4);
-  return u32x4{BF16::pack2(f[0], f[1]), BF16::pack2(f[2], f[3]), BF16::pack2(f[4], f[5]),
-               BF16::pack2(f[6], f[7])};
+  return u32x4{T::pack2(f[0], f[1]), T::pack2(f[2], f[3]), T::pack2(f[4], f[5]),
+               T::pack2(f[6], f[7])};
 }
 
-template <bool SWIGLU, bool GATHER, int BN>
+template <typename T, bool SWIGLU, bool GATHER, int BN>
 __global__ __launch_bounds__(256) void grouped_mfma_kernel(GemmArgs a) {
   constexpr int TN = BN / 4;       // columns per wave
   constexpr int MI = kGBM / 16;    // row sub-tiles
@@ -290,11 +299,12 @@ __global__ __launch_bounds__(256) void grouped_mfma_kernel(GemmArgs a) {
   const int wn = tid >> 6;
   int mt, nt;
   if (!xcd_tile(a, mt, nt)) return;
-  const int64_t e = a.table[mt * 3];
-  const int64_t start = a.table[mt * 3 + 1];
-  const int64_t stop = a.table[mt * 3 + 2];
-  if (start >= stop) return;
-  const int rows = (int)min((int64_t)a.tile_rows, stop - start);
+  const TileBounds tb = tile_bounds(a.table[mt * 3], a.table[mt * 3 + 1], a.table[mt * 3 + 2],
+                                    a.experts, a.y_rows, a.tile_rows);
+  if (tb.rows <= 0) return;
+  const int64_t e = tb.expert;
+  const int64_t start = tb.start;
+  const int rows = tb.rows;
   const int msub = (rows + 15) >> 4;  // live row sub-tiles
   const int8_t *wq = a.q + e * a.q_es;
   const float *wsc = a.s + e * a.s_es;
@@ -328,7 +338,7 @@ __global__ __launch_bounds__(256) void grouped_mfma_kernel(GemmArgs a) {
     const int c = tid + 256 * i;
     const int r = c >> 3;
     aok[i] = r < rows;
-    const int64_t xr = aok[i] ? (GATHER ? a.pos[start + r] : start + r) : 0;
+    const int64_t xr = aok[i] ? (GATHER ? clamp_index(a.pos[start + r], a.x_rows) : start + r) : 0;
     asrc[i] = a.x + xr * a.ldx + (c & 7) * 8;
   }
   const int8_t *bsrc[BCH];
@@ -394,7 +404,7 @@ __global__ __launch_bounds__(256) void grouped_mfma_kernel(GemmArgs a) {
       u32x4 bfr[NI];
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni)
-        bfr[ni] = dequant8_bf16(
+        bfr[ni] = dequant8<T>(
             *reinterpret_cast<const uint2 *>(&Bs[(col_base(ni) + (lane & 15)) * kLDB + kk]),
             sc[ni]);
 #pragma unroll
@@ -404,7 +414,7 @@ __global__ __launch_bounds__(256) void grouped_mfma_kernel(GemmArgs a) {
               *reinterpret_cast<const u32x4 *>(&As[(mi * 16 + (lane & 15)) * kLDA + kk]);
 #pragma unroll
           for (int ni = 0; ni < NI; ++ni)
-            acc[mi][ni] = BF16::mfma16x16x32(af, bfr[ni], acc[mi][ni]);
+            acc[mi][ni] = T::mfma16x16x32(af, bfr[ni], acc[mi][ni]);
         }
       }
     }
@@ -423,16 +433,16 @@ __global__ __launch_bounds__(256) void grouped_mfma_kernel(GemmArgs a) {
         for (int ni = 0; ni < NI / 2; ++ni) {
           const int col = n0 + wn * (TN / 2) + ni * 16 + (lane & 15);
           if (col < half) {
-            const float gate = round_bf16(acc[mi][ni][it]);
-            const float up = round_bf16(acc[mi][ni + NI / 2][it]);
-            yrow[col] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
+            const float gate = T::round(acc[mi][ni][it]);
+            const float up = T::round(acc[mi][ni + NI / 2][it]);
+            yrow[col] = T::from_f32(T::round(silu_f32(gate)) * up);
           }
         }
       } else {
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
           const int col = n0 + col_base(ni) + (lane & 15);
-          if (col < a.N) yrow[col] = f32_to_bf16_bits(acc[mi][ni][it]);
+          if (col < a.N) yrow[col] = T::from_f32(acc[mi][ni][it]);
         }
       }
     }
@@ -483,7 +493,8 @@ __device__ __forceinline__ int rb_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); 
 // lane quad reads 64 HL contiguous bytes of a weight row.  Weights are
 // requested BD - 1 stages ahead, activation rows AD stages ahead (AD - 1
 // stages wait in registers, one more in LDS).
-template <bool SWIGLU, bool GATHER, int K, int BM, int TN, int BD, int HL, int AD, int NW, int MS>
+template <typename T, bool SWIGLU, bool GATHER, int K, int BM, int TN, int BD, int HL, int AD, int NW,
+          int MS>
 __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t start, int rows,
                                         int nt, unsigned char *smem) {
   constexpr int KS = 64 * HL;
@@ -557,7 +568,7 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   for (int j = 0; j < A_W; ++j) {
     const int r = RPL * (NW * j + wave) + lane / CPR;
     const int rr = min(r, rows - 1);
-    const int64_t xr = GATHER ? a.pos[start + rr] : start + rr;
+    const int64_t xr = GATHER ? clamp_index(a.pos[start + rr], a.x_rows) : start + rr;
     asrc[j] = a.x + xr * a.ldx + (((lane % CPR) ^ rb_swz(r)) * 8);
   }
 
@@ -618,7 +629,7 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
       const float sc = scl[g * BN + col_base(ni) + (lane & 15)];
-      out[ni] = dequant8s_bf16(
+      out[ni] = dequant8s<T>(
           uint2{breg[ub][ni][p >> 1][2 * (p & 1)], breg[ub][ni][p >> 1][2 * (p & 1) + 1]}, sc);
     }
   };
@@ -657,7 +668,7 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
       for (int mi = 0; mi < MS; ++mi)
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni)
-          acc[mi][ni] = BF16::mfma16x16x32(af[mi], bcur[ni], acc[mi][ni]);
+          acc[mi][ni] = T::mfma16x16x32(af[mi], bcur[ni], acc[mi][ni]);
       __builtin_amdgcn_sched_group_barrier(0x100, MS, 0);
       if (nxt) __builtin_amdgcn_sched_group_barrier(0x002, 2 * VG, 0);
 #pragma unroll
@@ -700,101 +711,88 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
         for (int ni = 0; ni < NI / 2; ++ni) {
           const int col = n0 + wave * (TN / 2) + ni * 16 + (lane & 15);
           if (col < half) {
-            const float gate = round_bf16(acc[mi][ni][it]);
-            const float up = round_bf16(acc[mi][ni + NI / 2][it]);
-            yrow[col] = f32_to_bf16_bits(round_bf16(silu_fast(gate)) * up);
+            const float gate = T::round(acc[mi][ni][it]);
+            const float up = T::round(acc[mi][ni + NI / 2][it]);
+            yrow[col] = T::from_f32(T::round(silu_fast(gate)) * up);
           }
         }
       } else {
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
           const int col = n0 + col_base(ni) + (lane & 15);
-          if (col < a.N) yrow[col] = f32_to_bf16_bits(acc[mi][ni][it]);
+          if (col < a.N) yrow[col] = T::from_f32(acc[mi][ni][it]);
         }
       }
     }
   }
 }
 
-template <bool SWIGLU, bool GATHER, int K, int BM, int TN, int BD, int HL, int AD, int NW, int OCC>
+template <typename T, bool SWIGLU, bool GATHER, int K, int BM, int TN, int BD, int HL, int AD,
+          int NW, int OCC>
 __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
   constexpr int SC_BYTES = NW * TN * (K / 128) * 4;
   __shared__ __align__(16) unsigned char smem[3 * BM * 128 * HL + SC_BYTES];
   int mt, nt;
   if (!xcd_tile(a, mt, nt)) return;
-  int64_t e = 0, start, stop;
+  int64_t e = 0, start;
+  int rows;
   if (a.table) {
-    e = a.table[mt * 3];
-    start = a.table[mt * 3 + 1];
-    stop = a.table[mt * 3 + 2];
+    const TileBounds tb = tile_bounds(a.table[mt * 3], a.table[mt * 3 + 1], a.table[mt * 3 + 2],
+                                      a.experts, a.y_rows, a.tile_rows);
+    e = tb.expert;
+    start = tb.start;
+    rows = tb.rows;
   } else {  // dense: row tile mt of an [M, K] matrix
     start = (int64_t)mt * BM;
-    stop = a.M;
+    rows = (int)min((int64_t)a.tile_rows, a.M - start);
   }
-  if (start >= stop) return;
-  const int rows = (int)min((int64_t)a.tile_rows, stop - start);
+  if (rows <= 0) return;
   static_assert(BM == 96, "row-count dispatch below covers 96-row tiles");
   if (rows > 80)
-    rb_tile<SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 6>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 6>(a, e, start, rows, nt, smem);
   else if (rows > 64)
-    rb_tile<SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 5>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 5>(a, e, start, rows, nt, smem);
   else if (rows > 32)
-    rb_tile<SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 4>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 4>(a, e, start, rows, nt, smem);
   else
-    rb_tile<SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem);
 }
 
-// Configuration of grouped_rb_kernel (compile-time; these values were chosen
-// by measurement on the 2048-token prefill chunk): columns per wave, weight
-// ring slots, 64-K pieces per stage, occupancy hint, activation prefetch
-// distance in stages, waves per workgroup.
-#ifndef LM_RB_TN
-#define LM_RB_TN 32
-#endif
-#ifndef LM_RB_BD
-#define LM_RB_BD 3
-#endif
-#ifndef LM_RB_HL
-#define LM_RB_HL 1
-#endif
-#ifndef LM_RB_OCC
-#define LM_RB_OCC 3
-#endif
-#ifndef LM_RB_AD
-#define LM_RB_AD 2
-#endif
-#ifndef LM_RB_NW
-#define LM_RB_NW 4
-#endif
+// Configuration of grouped_rb_kernel, chosen by measurement on the
+// 2048-token prefill chunk: 4 waves of 32 columns each, a 3-slot weight ring
+// of one 64-K piece per stage, activations prefetched 2 stages ahead, a
+// register budget for 3 workgroups per CU.
+constexpr int kRbTN = 32;
+constexpr int kRbBD = 3;
+constexpr int kRbHL = 1;
+constexpr int kRbOcc = 3;
+constexpr int kRbAD = 2;
+constexpr int kRbNW = 4;
+constexpr int kGroupedBN = 128;  // grouped_mfma_kernel tile columns
 
-
-#ifndef LM_GROUPED_BN
-#define LM_GROUPED_BN 128
-#endif
-
-template <bool SWIGLU, bool GATHER>
+template <typename T, bool SWIGLU, bool GATHER>
 static int launch_grouped(GemmArgs a, unsigned mtiles, hipStream_t st) {
   if (mtiles == 0) return LM_OK;
   if (a.tile_rows <= 96 && (a.K == 2048 || a.K == 512)) {
-    constexpr int RBN = LM_RB_NW * LM_RB_TN;
+    constexpr int RBN = kRbNW * kRbTN;
     a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, RBN / 2) : (int)cdiv(a.N, RBN);
     a.mt_count = (int)mtiles;
     const int64_t grid = xcd_grid(a.mt_count, a.nt_count);
     LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
     if (a.K == 2048)
-      grouped_rb_kernel<SWIGLU, GATHER, 2048, 96, LM_RB_TN, LM_RB_BD, LM_RB_HL, LM_RB_AD, LM_RB_NW,
-                        LM_RB_OCC><<<(unsigned)grid, LM_RB_NW * 64, 0, st>>>(a);
+      grouped_rb_kernel<T, SWIGLU, GATHER, 2048, 96, kRbTN, kRbBD, kRbHL, kRbAD, kRbNW, kRbOcc>
+          <<<(unsigned)grid, kRbNW * 64, 0, st>>>(a);
     else
-      grouped_rb_kernel<SWIGLU, GATHER, 512, 96, LM_RB_TN, LM_RB_BD, LM_RB_HL, LM_RB_AD, LM_RB_NW,
-                        LM_RB_OCC><<<(unsigned)grid, LM_RB_NW * 64, 0, st>>>(a);
+      grouped_rb_kernel<T, SWIGLU, GATHER, 512, 96, kRbTN, kRbBD, kRbHL, kRbAD, kRbNW, kRbOcc>
+          <<<(unsigned)grid, kRbNW * 64, 0, st>>>(a);
     return check_launch("grouped_rb_kernel");
   }
-  constexpr int BN = LM_GROUPED_BN;
+  constexpr int BN = kGroupedBN;
   a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, BN / 2) : (int)cdiv(a.N, BN);
   a.mt_count = (int)mtiles;
   const int64_t grid = xcd_grid(a.mt_count, a.nt_count);
-    LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
-  grouped_mfma_kernel<SWIGLU, GATHER, BN><<<(unsigned)grid, 256, 0, st>>>(a);
+  LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
+  grouped_mfma_kernel<T, SWIGLU, GATHER, BN><<<(unsigned)grid, 256, 0, st>>>(a);
   return check_launch("grouped_mfma_kernel");
 }
 
@@ -823,41 +821,50 @@ int w8a16_gemm_dense(const void *x, const int8_t *q, const float *s, void *y, in
   a.N = (int)n;
   a.K = (int)k;
   (void)large_tile;
-  // bf16 rows at the model's K: the register-streamed kernel over 96-row
-  // tiles of the dense matrix (no tile table), faster than the LDS-dequant
-  // kernel because each wave dequantizes only its own columns' weights.
-  if (dtype == LM_BF16 && (k == 2048 || k == 512)) {
+  // Rows at the model's K: the register-streamed kernel over 96-row tiles of
+  // the dense matrix (no tile table), faster than the LDS-dequant kernel
+  // because each wave dequantizes only its own columns' weights.
+  if (k == 2048 || k == 512) {
     a.tile_rows = 96;
-    return launch_grouped<false, false>(a, cdiv(m, 96), st);
+    return dtype == LM_BF16 ? launch_grouped<BF16, false, false>(a, cdiv(m, 96), st)
+                            : launch_grouped<FP16, false, false>(a, cdiv(m, 96), st);
   }
   const unsigned mt = cdiv(m, 128);
   if (dtype == LM_BF16) return launch_gemm<BF16, 128, 2, false, false, true>(a, mt, st);
   return launch_gemm<FP16, 128, 2, false, false, true>(a, mt, st);
 }
 
-// Routed grouped GEMM over a (expert, start, stop) tile table of height bm.
-int routed_gemm(const void *x, const int8_t *q, const float *s, const int64_t *pos,
-                const int64_t *table, int64_t n_tiles, int64_t bm, void *y, int64_t n, int64_t k,
-                bool gather, bool swiglu, int64_t q_es, int64_t s_es, int64_t ldx,
-                hipStream_t st) {
-  GemmArgs a{};
-  a.x = static_cast<const uint16_t *>(x);
-  a.ldx = ldx;
-  a.pos = pos;
-  a.table = table;
-  a.q = q;
-  a.q_es = q_es;
-  a.s = s;
-  a.s_es = s_es;
-  a.y = static_cast<uint16_t *>(y);
-  a.ldy = swiglu ? n / 2 : n;
-  a.N = (int)n;
-  a.K = (int)k;
-  a.tile_rows = (int)bm;
-  const unsigned mt = (unsigned)n_tiles;
+template <typename T>
+static int routed_dispatch(const GemmArgs &a, unsigned mt, bool gather, bool swiglu,
+                           hipStream_t st) {
   if (swiglu)
-    return gather ? launch_grouped<true, true>(a, mt, st) : launch_grouped<true, false>(a, mt, st);
-  return gather ? launch_grouped<false, true>(a, mt, st) : launch_grouped<false, false>(a, mt, st);
+    return gather ? launch_grouped<T, true, true>(a, mt, st)
+                  : launch_grouped<T, true, false>(a, mt, st);
+  return gather ? launch_grouped<T, false, true>(a, mt, st)
+                : launch_grouped<T, false, false>(a, mt, st);
+}
+
+int routed_gemm(const RoutedGemm &r, hipStream_t st) {
+  GemmArgs a{};
+  a.x = static_cast<const uint16_t *>(r.x);
+  a.ldx = r.ldx;
+  a.pos = r.pos;
+  a.table = r.table;
+  a.experts = r.experts;
+  a.y_rows = r.y_rows;
+  a.x_rows = r.x_rows;
+  a.q = r.q;
+  a.q_es = r.q_es;
+  a.s = r.s;
+  a.s_es = r.s_es;
+  a.y = static_cast<uint16_t *>(r.y);
+  a.ldy = r.swiglu ? r.n / 2 : r.n;
+  a.N = (int)r.n;
+  a.K = (int)r.k;
+  a.tile_rows = (int)r.bm;
+  const unsigned mt = (unsigned)r.n_tiles;
+  return r.dtype == LM_BF16 ? routed_dispatch<BF16>(a, mt, r.gather, r.swiglu, st)
+                            : routed_dispatch<FP16>(a, mt, r.gather, r.swiglu, st);
 }
 
 int w8a16_gemv_dense(const void *x, const int8_t *q, const float *s, void *y, int64_t m,
@@ -876,39 +883,51 @@ extern "C" int lm_w8a16_linear(const void *x, const int8_t *q, const float *s, v
   if (m == 0) return LM_OK;
   LM_REQUIRE(x && q && s && y, LM_EINVAL, "null pointer");
   if (m <= 8) return w8a16_gemv_dense(x, q, s, y, m, n, k, dtype, as_stream(stream));
-  LM_REQUIRE(m < (1LL << 31) / 1, LM_EINVAL, "Invalid INT8 group geometry");
+  LM_REQUIRE(m < (1LL << 31), LM_EINVAL, "Invalid INT8 group geometry");
   return w8a16_gemm_dense(x, q, s, y, m, n, k, dtype, large_tile, as_stream(stream));
 }
 
-static int check_routed(const void *x, const int8_t *q, const float *s, const int64_t *table,
-                        int64_t n_tiles, int64_t bm, void *y, int64_t n, int64_t k) {
-  LM_REQUIRE(k > 0 && k % 128 == 0 && n > 0 && n < (1LL << 30), LM_EINVAL,
+static int check_routed(const RoutedGemm &r) {
+  LM_REQUIRE(r.dtype == LM_BF16 || r.dtype == LM_FP16, LM_EINVAL,
+             "W8A16 requires CUDA FP16/BF16 activations");
+  LM_REQUIRE(r.k > 0 && r.k % 128 == 0 && r.n > 0 && r.n < (1LL << 30), LM_EINVAL,
              "Invalid INT8 group geometry");
-  LM_REQUIRE(bm >= 1 && bm <= 128, LM_EINVAL, "tile height must be in 1..128");
-  LM_REQUIRE(n_tiles >= 0 && n_tiles < 65536, LM_EINVAL, "too many tiles");
-  LM_REQUIRE(n_tiles == 0 || (x && q && s && table && y), LM_EINVAL, "null pointer");
+  LM_REQUIRE(r.bm >= 1 && r.bm <= 128, LM_EINVAL, "tile height must be in 1..128");
+  LM_REQUIRE(r.n_tiles >= 0 && r.n_tiles < 65536, LM_EINVAL, "too many tiles");
+  LM_REQUIRE(r.experts >= 1 && r.y_rows >= 0 && r.x_rows >= 0, LM_EINVAL,
+             "invalid bank or row count");
+  if (r.n_tiles == 0 || r.y_rows == 0) return LM_OK;
+  LM_REQUIRE(r.x && r.q && r.s && r.table && r.y, LM_EINVAL, "null pointer");
+  LM_REQUIRE(r.x_rows >= 1, LM_EINVAL, "no activation rows");
+  LM_REQUIRE(!r.gather || r.pos, LM_EINVAL, "gather needs pos");
+  // contiguous rows: output row p reads activation row p
+  LM_REQUIRE(r.gather || r.y_rows <= r.x_rows, LM_EINVAL, "more output rows than activation rows");
   return LM_OK;
 }
 
-extern "C" int lm_routed_gemm_w8a16(const void *x, const int8_t *q, const float *s,
-                                    const int64_t *pos, const int64_t *table, int64_t n_tiles,
-                                    int64_t bm, void *y, int64_t n, int64_t k, int gather,
-                                    int64_t q_expert_stride, int64_t s_expert_stride,
+extern "C" int lm_routed_gemm_w8a16(const void *x, int64_t x_rows, const int8_t *q, const float *s,
+                                    int64_t experts, int64_t q_expert_stride,
+                                    int64_t s_expert_stride, const int64_t *pos,
+                                    const int64_t *table, int64_t n_tiles, int64_t bm, void *y,
+                                    int64_t y_rows, int64_t n, int64_t k, int gather, int dtype,
                                     void *stream) {
-  if (int rc = check_routed(x, q, s, table, n_tiles, bm, y, n, k)) return rc;
-  LM_REQUIRE(!gather || pos || n_tiles == 0, LM_EINVAL, "gather needs pos");
-  return routed_gemm(x, q, s, pos, table, n_tiles, bm, y, n, k, gather != 0, false,
-                     q_expert_stride, s_expert_stride, k, as_stream(stream));
+  RoutedGemm r{x, k, x_rows, q, s, q_expert_stride, s_expert_stride, experts, pos, table,
+               n_tiles, bm, y, y_rows, n, k, gather != 0, false, dtype};
+  if (int rc = check_routed(r)) return rc;
+  if (n_tiles == 0 || y_rows == 0) return LM_OK;
+  return routed_gemm(r, as_stream(stream));
 }
 
-extern "C" int lm_routed_gate_up_swiglu(const void *x, const int8_t *q, const float *s,
-                                        const int64_t *pos, const int64_t *table,
-                                        int64_t n_tiles, int64_t bm, void *h, int64_t n, int64_t k,
-                                        int64_t q_expert_stride, int64_t s_expert_stride,
+extern "C" int lm_routed_gate_up_swiglu(const void *x, int64_t x_rows, const int8_t *q,
+                                        const float *s, int64_t experts, int64_t q_expert_stride,
+                                        int64_t s_expert_stride, const int64_t *pos,
+                                        const int64_t *table, int64_t n_tiles, int64_t bm,
+                                        void *h, int64_t h_rows, int64_t n, int64_t k, int dtype,
                                         void *stream) {
-  if (int rc = check_routed(x, q, s, table, n_tiles, bm, h, n, k)) return rc;
+  RoutedGemm r{x, k, x_rows, q, s, q_expert_stride, s_expert_stride, experts, pos, table,
+               n_tiles, bm, h, h_rows, n, k, true, true, dtype};
+  if (int rc = check_routed(r)) return rc;
   LM_REQUIRE(n % 2 == 0, LM_EINVAL, "gate_up needs an even number of rows");
-  LM_REQUIRE(pos || n_tiles == 0, LM_EINVAL, "gather needs pos");
-  return routed_gemm(x, q, s, pos, table, n_tiles, bm, h, n, k, true, true, q_expert_stride,
-                     s_expert_stride, k, as_stream(stream));
+  if (n_tiles == 0 || h_rows == 0) return LM_OK;
+  return routed_gemm(r, as_stream(stream));
 }

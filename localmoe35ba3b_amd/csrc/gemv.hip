@@ -73,7 +73,8 @@ __device__ __forceinline__ Resolved resolve(const GemvArgs &a) {
 }
 
 // LDS carve-up: [xq or x16 | xs | ws | partials]
-template <int MT, bool QUANT, bool PARTIALS>
+// T: dtype of the activations (QUANT) and of the output.
+template <typename T, int MT, bool QUANT, bool PARTIALS>
 __global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const Resolved rv = resolve(a);
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
   const int th = threadIdx.x;
   if (rv.rvalid * G <= kGemvLoads * 8 * (kGemvThreads / 64) && M * G <= kGemvThreads &&
       (QUANT ? M * G <= QJ * (kGemvThreads / 32) : M * K <= XN * 16 * kGemvThreads)) {
-    QuantStage<BF16, QJ> qst;
+    QuantStage<T, QJ> qst;
     RowStage<XN> cst;
     if constexpr (QUANT)
       qst.load(a.x + (int64_t)rv.xrow * a.ldx, a.ldx, M, K);
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
   } else {
     // Activations: quantize bf16 rows, or copy pre-quantized rows.
     if constexpr (QUANT) {
-      quantize_rows_to_lds<BF16>(a.x + (int64_t)rv.xrow * a.ldx, a.ldx, M, K, xq, xs);
+      quantize_rows_to_lds<T>(a.x + (int64_t)rv.xrow * a.ldx, a.ldx, M, K, xq, xs);
     } else {
       for (int i = threadIdx.x; i < M * K / 16; i += blockDim.x) {
         const int m = (i * 16) / K, c = (i * 16) - m * K;
@@ -171,17 +172,17 @@ __global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
       const int rh = rv.rvalid >> 1;
       for (int i = threadIdx.x; i < M * rh; i += blockDim.x) {
         const int m = i / rh, t = i - m * rh;
-        const float gate = round_bf16(w8a8_epilogue(part + m * RG + t * G, xs + m * G, ws + t * G, G));
+        const float gate = T::round(w8a8_epilogue(part + m * RG + t * G, xs + m * G, ws + t * G, G));
         const float up =
-            round_bf16(w8a8_epilogue(part + m * RG + (rh + t) * G, xs + m * G, ws + (rh + t) * G, G));
-        const float act = round_bf16(silu_f32(gate));
-        a.y[(int64_t)(rv.yrow + m) * a.ldy + rv.n0 + t] = f32_to_bf16_bits(act * up);
+            T::round(w8a8_epilogue(part + m * RG + (rh + t) * G, xs + m * G, ws + (rh + t) * G, G));
+        const float act = T::round(silu_f32(gate));
+        a.y[(int64_t)(rv.yrow + m) * a.ldy + rv.n0 + t] = T::from_f32(act * up);
       }
     } else {
       for (int i = threadIdx.x; i < M * rv.rvalid; i += blockDim.x) {
         const int m = i / rv.rvalid, t = i - m * rv.rvalid;
         const float acc = w8a8_epilogue(part + m * RG + t * G, xs + m * G, ws + t * G, G);
-        a.y[(int64_t)(rv.yrow + m) * a.ldy + rv.n0 + t] = f32_to_bf16_bits(acc);
+        a.y[(int64_t)(rv.yrow + m) * a.ldy + rv.n0 + t] = T::from_f32(acc);
       }
     }
   }
@@ -270,25 +271,30 @@ static int gemv_rows_per_block(int64_t k) {
 
 static int mt_for(int64_t m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; }
 
-template <int MT, bool QUANT, bool PARTIALS>
+template <typename T, int MT, bool QUANT, bool PARTIALS>
 static int launch_w8a8(const GemvArgs &a, unsigned gy, hipStream_t st) {
   const int G = a.K / 128;
   const size_t lds = (size_t)MT * a.K + (size_t)MT * G * 4 + (size_t)a.RB * G * 4 +
                      (size_t)MT * a.RB * G * 4;
   LM_REQUIRE(lds <= 160 * 1024, LM_EINVAL, "Invalid INT8 group geometry");
   const unsigned gx = a.swiglu ? cdiv(a.N / 2, a.RB / 2) : cdiv(a.N, a.RB);
-  w8a8_gemv_kernel<MT, QUANT, PARTIALS><<<dim3(gx, gy), kGemvThreads, lds, st>>>(a);
+  w8a8_gemv_kernel<T, MT, QUANT, PARTIALS><<<dim3(gx, gy), kGemvThreads, lds, st>>>(a);
   return check_launch("w8a8_gemv_kernel");
 }
 
-template <bool QUANT, bool PARTIALS>
-static int dispatch_w8a8(const GemvArgs &a, unsigned gy, hipStream_t st) {
+template <typename T, bool QUANT, bool PARTIALS>
+static int dispatch_w8a8_t(const GemvArgs &a, unsigned gy, hipStream_t st) {
   switch (mt_for(a.M)) {
-    case 1: return launch_w8a8<1, QUANT, PARTIALS>(a, gy, st);
-    case 2: return launch_w8a8<2, QUANT, PARTIALS>(a, gy, st);
-    case 4: return launch_w8a8<4, QUANT, PARTIALS>(a, gy, st);
-    default: return launch_w8a8<8, QUANT, PARTIALS>(a, gy, st);
+    case 1: return launch_w8a8<T, 1, QUANT, PARTIALS>(a, gy, st);
+    case 2: return launch_w8a8<T, 2, QUANT, PARTIALS>(a, gy, st);
+    case 4: return launch_w8a8<T, 4, QUANT, PARTIALS>(a, gy, st);
+    default: return launch_w8a8<T, 8, QUANT, PARTIALS>(a, gy, st);
   }
+}
+template <bool QUANT, bool PARTIALS>
+static int dispatch_w8a8(const GemvArgs &a, int dtype, unsigned gy, hipStream_t st) {
+  return dtype == LM_FP16 ? dispatch_w8a8_t<FP16, QUANT, PARTIALS>(a, gy, st)
+                          : dispatch_w8a8_t<BF16, QUANT, PARTIALS>(a, gy, st);
 }
 
 template <typename T, int MT>
@@ -339,10 +345,16 @@ static int check_grouped(int64_t experts, int64_t n, int64_t k, int field) {
   return LM_OK;
 }
 
+static int check_dtype(int dtype, const char *msg) {
+  LM_REQUIRE(dtype == LM_BF16 || dtype == LM_FP16, LM_EINVAL, msg);
+  return LM_OK;
+}
+
 extern "C" int lm_w8a8_grouped_gemv(const int8_t *xq, const float *xs, const int64_t *table,
                                     void *y, int64_t experts, int64_t n, int64_t k, int field,
-                                    int shared, void *stream) {
+                                    int shared, int y_dtype, void *stream) {
   if (int rc = check_grouped(experts, n, k, field)) return rc;
+  if (int rc = check_dtype(y_dtype, "W8A8 output must be bf16 or fp16")) return rc;
   if (experts == 0) return LM_OK;
   LM_REQUIRE(xq && xs && table && y, LM_EINVAL, "null pointer");
   GemvArgs a{};
@@ -357,13 +369,14 @@ extern "C" int lm_w8a8_grouped_gemv(const int8_t *xq, const float *xs, const int
   a.N = (int)n;
   a.K = (int)k;
   a.RB = gemv_rows_per_block(k);
-  return dispatch_w8a8<false, false>(a, (unsigned)experts, as_stream(stream));
+  return dispatch_w8a8<false, false>(a, y_dtype, (unsigned)experts, as_stream(stream));
 }
 
 extern "C" int lm_w8a8_grouped_linear(const void *x, const int64_t *table, void *y,
                                       int64_t experts, int64_t n, int64_t k, int field,
-                                      int shared, void *stream) {
+                                      int shared, int dtype, void *stream) {
   if (int rc = check_grouped(experts, n, k, field)) return rc;
+  if (int rc = check_dtype(dtype, "Expected CUDA rows with K divisible by 128")) return rc;
   if (experts == 0) return LM_OK;
   LM_REQUIRE(x && table && y, LM_EINVAL, "null pointer");
   GemvArgs a{};
@@ -378,15 +391,16 @@ extern "C" int lm_w8a8_grouped_linear(const void *x, const int64_t *table, void 
   a.N = (int)n;
   a.K = (int)k;
   a.RB = gemv_rows_per_block(k);
-  return dispatch_w8a8<true, false>(a, (unsigned)experts, as_stream(stream));
+  return dispatch_w8a8<true, false>(a, dtype, (unsigned)experts, as_stream(stream));
 }
 
 extern "C" int lm_w8a8_linear(const void *x, const int8_t *q, const float *s, void *y, int64_t m,
-                              int64_t n, int64_t k, int swiglu, void *stream) {
+                              int64_t n, int64_t k, int swiglu, int dtype, void *stream) {
   LM_REQUIRE(m >= 0 && m <= 8, LM_EINVAL, "W8A8 decode linear supports 1..8 rows");
   LM_REQUIRE(n > 0 && k > 0 && k % 128 == 0 && k <= 65536, LM_EINVAL,
              "Invalid INT8 group geometry");
   LM_REQUIRE(!swiglu || n % 2 == 0, LM_EINVAL, "SwiGLU needs an even number of rows");
+  if (int rc = check_dtype(dtype, "Expected CUDA rows with K divisible by 128")) return rc;
   if (m == 0) return LM_OK;
   LM_REQUIRE(x && q && s && y, LM_EINVAL, "null pointer");
   GemvArgs a{};
@@ -401,7 +415,7 @@ extern "C" int lm_w8a8_linear(const void *x, const int8_t *q, const float *s, vo
   a.K = (int)k;
   a.RB = gemv_rows_per_block(k);
   a.swiglu = swiglu ? 1 : 0;
-  return dispatch_w8a8<true, false>(a, 1, as_stream(stream));
+  return dispatch_w8a8<true, false>(a, dtype, 1, as_stream(stream));
 }
 
 extern "C" int lm_w8a8_group_partials(const int8_t *xq, const int8_t *wq, int32_t *p, int64_t m,
@@ -420,13 +434,14 @@ extern "C" int lm_w8a8_group_partials(const int8_t *xq, const int8_t *wq, int32_
   a.N = (int)n;
   a.K = (int)k;
   a.RB = gemv_rows_per_block(k);
-  return dispatch_w8a8<false, true>(a, 1, as_stream(stream));
+  return dispatch_w8a8<false, true>(a, LM_BF16, 1, as_stream(stream));
 }
 
 extern "C" int lm_w8a16_grouped_gemv(const void *x, const int64_t *table, void *y,
                                      int64_t experts, int64_t n, int64_t k, int field, int shared,
-                                     void *stream) {
+                                     int dtype, void *stream) {
   if (int rc = check_grouped(experts, n, k, field)) return rc;
+  if (int rc = check_dtype(dtype, "W8A16 requires CUDA FP16/BF16 activations")) return rc;
   if (experts == 0) return LM_OK;
   LM_REQUIRE(x && table && y, LM_EINVAL, "null pointer");
   GemvArgs a{};
@@ -441,5 +456,6 @@ extern "C" int lm_w8a16_grouped_gemv(const void *x, const int64_t *table, void *
   a.N = (int)n;
   a.K = (int)k;
   a.RB = gemv_rows_per_block(k);
-  return dispatch_w8a16<BF16>(a, (unsigned)experts, as_stream(stream));
+  return dtype == LM_FP16 ? dispatch_w8a16<FP16>(a, (unsigned)experts, as_stream(stream))
+                          : dispatch_w8a16<BF16>(a, (unsigned)experts, as_stream(stream));
 }

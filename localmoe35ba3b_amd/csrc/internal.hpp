@@ -13,9 +13,24 @@ int router_topk(const float *logits, int64_t T, int64_t E, int64_t K, int64_t *i
 int route_plan(const int64_t *ids, int64_t T, int64_t K, int64_t E, int64_t bm, int64_t *pos,
                int64_t *table, int64_t max_tiles, int64_t *ordered, int64_t *slots,
                int64_t shared_rows, hipStream_t st);
-int routed_gemm(const void *x, const int8_t *q, const float *s, const int64_t *pos,
-                const int64_t *table, int64_t n_tiles, int64_t bm, void *y, int64_t n, int64_t k,
-                bool gather, bool swiglu, int64_t q_es, int64_t s_es, int64_t ldx,
-                hipStream_t st);
+// One routed grouped W8A16 GEMM (gate_up with gather + optional SwiGLU
+// epilogue, or down over contiguous rows) over a (expert, start, stop) tile
+// table.  Table experts are clamped into [0, experts), starts and stops into
+// [0, y_rows], gathered row indices into [0, x_rows).
+struct RoutedGemm {
+  const void *x;
+  int64_t ldx, x_rows;
+  const int8_t *q;
+  const float *s;
+  int64_t q_es, s_es, experts;
+  const int64_t *pos;
+  const int64_t *table;
+  int64_t n_tiles, bm;
+  void *y;
+  int64_t y_rows, n, k;
+  bool gather, swiglu;
+  int dtype;
+};
+int routed_gemm(const RoutedGemm &r, hipStream_t st);
 
 }  // namespace lm

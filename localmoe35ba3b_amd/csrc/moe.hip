@@ -18,6 +18,8 @@
 // per-workgroup expert counts, the route plan scan (with the shared expert
 // appended as extra tiles), grouped W8A16 gate_up GEMM with fused SwiGLU,
 // grouped W8A16 down GEMM, and a per-token combine.
+#include <algorithm>
+
 #include "gemv_core.hpp"
 #include "internal.hpp"
 
@@ -32,7 +34,7 @@ constexpr int kTopkTokens = 8;  // prefill top-k: tokens (waves) per workgroup
 static_assert(kE == 256, "the prefill kernels map one thread of a 256-thread workgroup to each expert");
 
 struct WsLayout {
-  int64_t ctr, bcounts, xn, gl, logits, nx, nw, ids, wts, sel, selw, xq, xs, pos, table, rslot,
+  int64_t bcounts, xn, gl, logits, nx, nw, ids, wts, sel, selw, xq, xs, pos, table, rslot,
       rpos, hbuf, vbuf, total;
   int64_t max_tiles, n_tiles;
 };
@@ -50,7 +52,6 @@ static WsLayout layout(int64_t T) {
     o = align256(o + bytes);
     return at;
   };
-  w.ctr = take(256);
   w.xn = take(T * kH * 2);
   w.gl = take(T * 4);
   w.logits = take(T * kE * 4);
@@ -86,7 +87,6 @@ struct LayerArgs {
   uint16_t *h;
   float eps;
   // workspace views
-  int *ctr;
   uint16_t *xn;
   float *gl;
   float *logits;
@@ -213,13 +213,11 @@ __device__ __forceinline__ void decode_topk(const LayerArgs &a, int *sel, float 
   const int t = threadIdx.x;
   if (t < 64) {
     topk_wave(a.logits, kE, kTopK, t, scratch, sid, swt);
-    __builtin_amdgcn_wave_barrier();
-    if (t < kTopK) {  // route t: its rank among the (distinct) ids is its combine slot
-      const int64_t id = sid[t];
+    wave_lds_sync();
+    if (t < kTopK) {  // route t: its rank in ascending id order is its combine slot
+      const int64_t id = clamp_index(sid[t], kE);
       const uint16_t wb = swt[t];
-      int rank = 0;
-#pragma unroll
-      for (int j = 0; j < kTopK; ++j) rank += sid[j] < id ? 1 : 0;
+      const int rank = combine_slot(sid, kTopK, t);
       const float w = bf16_bits_to_f32(wb);
       sel[rank] = (int)id;
       selw[rank] = w;
@@ -280,7 +278,7 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
   }
   if (!shared) {
     decode_topk(a, sel, selw);
-    issue(sel[slot]);
+    issue(clamp_index32(sel[slot], kE));
   }
   if (shared) {
     reinterpret_cast<u32x4 *>(xbuf)[t] = xv;
@@ -337,18 +335,10 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   __shared__ float selw[kTopK];
   const int t = threadIdx.x;
   const int c0 = blockIdx.x * kDnCols;
-  int ex[kTopK + 1];
+  int ex[kTopK];
 #pragma unroll
   for (int s = 0; s < kTopK; ++s) ex[s] = a.sel[s];
-  ex[kTopK] = kE;
-  auto expert_of = [&](int r) {
-    const int s = r / kDnCols;
-    int e = kE;
-#pragma unroll
-    for (int j = 0; j < kTopK; ++j)
-      if (s == j) e = ex[j];
-    return e;
-  };
+  auto expert_of = [&](int r) { return decode_row_expert(ex, kTopK, kDnCols, kE, r); };
   // The SwiGLU rows are requested together with the expert ids; the weight
   // loads follow as soon as the ids arrive.
   const int row = t >> 5, col = (t & 31) * 16;
@@ -561,9 +551,7 @@ router_approx_kernel(LayerArgs a, int T) {
     for (int j = 0; j < NLD; ++j)
       *reinterpret_cast<u32x4 *>(my + (4 * j + lr) * PITCH + lc * 16) = rg[j];
     // the segment is read across lanes: every lane's stores come first
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_lds_sync();
     if (ss + 1 < NSS) gload(ss + 1);
 #pragma unroll
     for (int st = 0; st < SS / 32; ++st) {  // 32-wide MFMA steps: values 32 st + 8 q .. + 7
@@ -580,7 +568,7 @@ router_approx_kernel(LayerArgs a, int T) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = BF16::mfma16x16x32(av[i], bv[j], acc[i][j]);
     }
-    __builtin_amdgcn_wave_barrier();  // every lane's reads before the next segment is stored
+    wave_lds_sync();  // every lane's reads before the next segment is stored
   }
   if (wave > 0) {
 #pragma unroll
@@ -664,7 +652,7 @@ __device__ void topk_exact_wave(const LayerArgs &a, int tok, int lane, unsigned 
     if (c) cand[n + before] = lane * 4 + j;
     n += __popcll(m);
   }
-  __builtin_amdgcn_wave_barrier();
+  wave_lds_sync();
   // exact logits, CB candidates per batch, the next batch's rows requested
   // before the current batch is reduced: lane holds x[k] and w[k] for
   // k = 8 lane + 512 i + (0..7)
@@ -712,7 +700,7 @@ __device__ void topk_exact_wave(const LayerArgs &a, int tok, int lane, unsigned 
     if (c0 + 2 * CB < n) fetch(0, c0 + 2 * CB);
     if (c0 + CB < n) reduce(1, c0 + CB);
   }
-  __builtin_amdgcn_wave_barrier();
+  wave_lds_sync();
   float v[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) v[j] = lv[lane * 4 + j];
@@ -730,7 +718,7 @@ __device__ void topk_exact_wave(const LayerArgs &a, int tok, int lane, unsigned 
   const float cv = has ? lv[ce] : 0.0f;
   const T ck = has ? KT::make(cv, ce) : (T)0;
   keys[lane] = ck;
-  __builtin_amdgcn_wave_barrier();
+  wave_lds_sync();
   int rank = 0;
   for (int c = 0; c < n; ++c) rank += keys[c] > ck ? 1 : 0;
   const unsigned long long first = __ballot(has && rank == 0);
@@ -748,7 +736,7 @@ __device__ void topk_exact_wave(const LayerArgs &a, int tok, int lane, unsigned 
   const bool chosen = has && rank < kTopK;
   const float pe = expf(KT::value(ck) - mx) / denom;
   if (chosen) prob[rank] = pe;
-  __builtin_amdgcn_wave_barrier();
+  wave_lds_sync();
   float psum = 0.0f;
 #pragma unroll
   for (int i = 0; i < kTopK; ++i) psum += prob[i];
@@ -792,9 +780,9 @@ __global__ __launch_bounds__(kTopkTokens * 64) void prefill_topk_count_kernel(La
       topk_exact_wave<Key64>(a, tok, lane, scratch[w], lv[w], cand[w], sid[w], swt[w]);
     else
       topk_exact_wave<Key32>(a, tok, lane, scratch[w], lv[w], cand[w], sid[w], swt[w]);
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_sync();
     if (lane < kTopK) {
-      e = (int)sid[w][lane];
+      e = (int)clamp_index(sid[w][lane], kE);
       a.ids[(int64_t)tok * kTopK + lane] = e;
       a.wts[(int64_t)tok * kTopK + lane] = swt[w][lane];
       rank = atomicAdd(&lcnt[e], 1);
@@ -824,7 +812,7 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
   const int t = threadIdx.x;
   const int R = T * kTopK;
   const int r = blockIdx.x * kScanRoutes + t;
-  const int e_r = r < R ? (int)ids[r] : 0;
+  const int e_r = r < R ? (int)clamp_index(ids[r], kE) : 0;
   const int s_r = r < R ? rslot[r] : 0;
   const int j0 = blockIdx.x * kScanGroups;
   {
@@ -873,7 +861,7 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
   __syncthreads();
   if (r < R) {
     const int jb = r / (kTopkTokens * kTopK) - j0;
-    const int p = offs[e_r] + bpre[jb][e_r] + s_r;
+    const int p = clamp_index32(offs[e_r] + bpre[jb][e_r] + s_r, R);
     pos[p] = r / kTopK;
     rpos[r] = p;
   }
@@ -920,8 +908,8 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(LayerArgs a, const
   float w[kTopK];
 #pragma unroll
   for (int i = 0; i < kTopK; ++i) {
-    e[i] = (int)a.ids[(int64_t)tok * kTopK + i];
-    p[i] = rpos[(int64_t)tok * kTopK + i];
+    e[i] = (int)clamp_index(a.ids[(int64_t)tok * kTopK + i], kE);
+    p[i] = clamp_index32(rpos[(int64_t)tok * kTopK + i], (int)R);
     w[i] = bf16_bits_to_f32(a.wts[(int64_t)tok * kTopK + i]);
   }
 #pragma unroll
@@ -975,9 +963,12 @@ __global__ void export_routing_kernel(const int64_t *ids, const uint16_t *wts, i
   if (wts_out) wts_out[i] = wts[i];
 }
 
+// Zeroes n bytes (n a multiple of 4) with a grid-stride loop of dword stores.
 __global__ void fill_zero_kernel(uint32_t *p, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n) p[i] = 0u;
+  const int64_t words = n >> 2;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < words;
+       i += (int64_t)gridDim.x * 256)
+    p[i] = 0u;
 }
 
 }  // namespace lm
@@ -990,9 +981,31 @@ extern "C" int64_t lm_moe_workspace_bytes(int64_t max_tokens, int64_t hidden, in
   return layout(max_tokens).total;
 }
 
+extern "C" int lm_moe_workspace_region(int64_t tokens, int region, int64_t *offset,
+                                       int64_t *bytes) {
+  LM_REQUIRE(tokens >= 1 && tokens <= 65536, LM_EINVAL, "invalid token count");
+  LM_REQUIRE(offset && bytes, LM_EINVAL, "null pointer");
+  const WsLayout w = layout(tokens);
+  const int64_t T = tokens, R = T * kTopK;
+  switch (region) {
+    case LM_WS_NORMED: *offset = w.xn; *bytes = T * kH * 2; break;
+    case LM_WS_GATE: *offset = w.gl; *bytes = T * 4; break;
+    case LM_WS_IDS: *offset = w.ids; *bytes = R * 8; break;
+    case LM_WS_WEIGHTS: *offset = w.wts; *bytes = R * 2; break;
+    case LM_WS_ROUTE_ROWS: *offset = w.rpos; *bytes = R * 4; break;
+    case LM_WS_HIDDEN: *offset = w.hbuf; *bytes = (R + T) * kI * 2; break;
+    case LM_WS_DOWN: *offset = w.vbuf; *bytes = (R + T) * kH * 2; break;
+    default: return set_error(LM_EINVAL, "unknown workspace region");
+  }
+  return LM_OK;
+}
+
 extern "C" int lm_moe_workspace_init(void *workspace, int64_t bytes, void *stream) {
-  LM_REQUIRE(workspace && bytes >= 256, LM_EINVAL, "workspace too small");
-  fill_zero_kernel<<<1, 256, 0, as_stream(stream)>>>(static_cast<uint32_t *>(workspace), 64);
+  LM_REQUIRE(workspace && bytes >= 256 && bytes % 4 == 0, LM_EINVAL,
+             "workspace must be at least 256 bytes and a multiple of 4");
+  const int64_t blocks = std::min<int64_t>(cdiv(bytes >> 2, 256), 4096);
+  fill_zero_kernel<<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
+      static_cast<uint32_t *>(workspace), bytes);
   return check_launch("fill_zero_kernel");
 }
 
@@ -1026,7 +1039,6 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   a.dn_ses = layer->dn_s_expert_stride;
   a.h = static_cast<uint16_t *>(h);
   a.eps = eps;
-  a.ctr = reinterpret_cast<int *>(ws + w.ctr);
   a.xn = reinterpret_cast<uint16_t *>(ws + w.xn);
   a.gl = reinterpret_cast<float *>(ws + w.gl);
   a.logits = reinterpret_cast<float *>(ws + w.logits);
@@ -1085,13 +1097,15 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
                                                               (int)w.max_tiles, pos, table, rpos);
   if (int rc = check_launch("prefill_scan_kernel")) return rc;
   if (int rc = mark(4)) return rc;
-  if (int rc = routed_gemm(a.xn, a.gu_q, a.gu_s, pos, table, w.n_tiles, kBM, a.hbuf, 2 * kI, kH,
-                           true, true, a.gu_qes, a.gu_ses, kH, st))
-    return rc;
+  // gate_up over the T token rows gathered through pos, down over the R + T
+  // rows of hbuf; the banks hold E + 1 experts (index E = shared expert)
+  const RoutedGemm gu{a.xn, kH, T, a.gu_q, a.gu_s, a.gu_qes, a.gu_ses, kE + 1, pos, table,
+                      w.n_tiles, kBM, a.hbuf, R + T, 2 * kI, kH, true, true, LM_BF16};
+  if (int rc = routed_gemm(gu, st)) return rc;
   if (int rc = mark(5)) return rc;
-  if (int rc = routed_gemm(a.hbuf, a.dn_q, a.dn_s, pos, table, w.n_tiles, kBM, vbuf, kH, kI, false,
-                           false, a.dn_qes, a.dn_ses, kI, st))
-    return rc;
+  const RoutedGemm dn{a.hbuf, kI, R + T, a.dn_q, a.dn_s, a.dn_qes, a.dn_ses, kE + 1, pos, table,
+                      w.n_tiles, kBM, vbuf, R + T, kH, kI, false, false, LM_BF16};
+  if (int rc = routed_gemm(dn, st)) return rc;
   if (int rc = mark(6)) return rc;
   prefill_combine_kernel<<<(unsigned)T, 256, 0, st>>>(a, rpos, vbuf, R);
   if (int rc = check_launch("prefill_combine_kernel")) return rc;

@@ -400,11 +400,14 @@ int route_plan(const int64_t *ids, int64_t T, int64_t K, int64_t E, int64_t bm, 
 
 // ============================================================ combines
 __device__ __forceinline__ float load_weight(const void *w, int dtype, int64_t i) {
-  return dtype == LM_FP32 ? static_cast<const float *>(w)[i]
-                          : bf16_bits_to_f32(static_cast<const uint16_t *>(w)[i]);
+  if (dtype == LM_FP32) return static_cast<const float *>(w)[i];
+  const uint16_t b = static_cast<const uint16_t *>(w)[i];
+  return dtype == LM_FP16 ? f16_bits_to_f32(b) : bf16_bits_to_f32(b);
 }
 
-// int8._ordered_reduce: ascending table order, bf16 rounding at every step.
+// int8._ordered_reduce: ascending table order, rounding to the output dtype T
+// at every step.  A table slot outside [0, E) is clamped into it.
+template <typename T>
 __global__ __launch_bounds__(256) void ordered_reduce_kernel(const uint16_t *__restrict__ v,
                                                              const int64_t *__restrict__ table,
                                                              const void *w, int w_dtype,
@@ -414,36 +417,39 @@ __global__ __launch_bounds__(256) void ordered_reduce_kernel(const uint16_t *__r
   if (n >= N) return;
   float acc = 0.0f;
   for (int e = 0; e < E; ++e) {
-    const int64_t slot = table[e * 5 + 4];
+    const int64_t slot = clamp_index(table[e * 5 + 4], E);
     const float wt = load_weight(w, w_dtype, slot);
-    const float val = round_bf16(bf16_bits_to_f32(v[(int64_t)e * N + n]) * wt);
-    acc = round_bf16(acc + val);
+    const float val = T::round(T::to_f32(v[(int64_t)e * N + n]) * wt);
+    acc = T::round(acc + val);
   }
-  y[n] = f32_to_bf16_bits(acc);
+  y[n] = T::from_f32(acc);
 }
 
-// prefill._reduce: per token, routes in ascending expert order.
+// prefill._reduce: per token, routes in ascending expert order, rounding to
+// T at every step.  Routes are clamped into [0, tokens * K), slots into [0, K).
+template <typename T>
 __global__ __launch_bounds__(256) void routed_reduce_kernel(const uint16_t *__restrict__ v,
                                                             const int64_t *__restrict__ ordered,
                                                             const int64_t *__restrict__ slots,
                                                             const void *w, int w_dtype,
                                                             uint16_t *__restrict__ y, int N,
-                                                            int K) {
+                                                            int K, int64_t routes) {
   const int tok = blockIdx.y;
   const int n = blockIdx.x * 256 + threadIdx.x;
   if (n >= N) return;
   float acc = 0.0f;
   for (int i = 0; i < K; ++i) {
-    const int64_t route = ordered[(int64_t)tok * K + i];
-    const int64_t slot = slots[(int64_t)tok * K + i];
+    const int64_t route = clamp_index(ordered[(int64_t)tok * K + i], routes);
+    const int64_t slot = clamp_index(slots[(int64_t)tok * K + i], K);
     const float wt = load_weight(w, w_dtype, (int64_t)tok * K + slot);
-    const float val = round_bf16(bf16_bits_to_f32(v[route * N + n]) * wt);
-    acc = round_bf16(acc + val);
+    const float val = T::round(T::to_f32(v[route * N + n]) * wt);
+    acc = T::round(acc + val);
   }
-  y[(int64_t)tok * N + n] = f32_to_bf16_bits(acc);
+  y[(int64_t)tok * N + n] = T::from_f32(acc);
 }
 
-// SwiGLU glue on a [rows, 2*half] bf16 gate_up tensor.
+// SwiGLU glue on a [rows, 2*half] gate_up tensor of dtype T.
+template <typename T>
 __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *__restrict__ gu,
                                                      uint16_t *__restrict__ h, int64_t rows,
                                                      int64_t half) {
@@ -451,9 +457,9 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t *__restrict_
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * 256) {
     const int64_t r = i / half, c = i - r * half;
-    const float g = bf16_bits_to_f32(gu[r * 2 * half + c]);
-    const float u = bf16_bits_to_f32(gu[r * 2 * half + half + c]);
-    h[i] = f32_to_bf16_bits(round_bf16(silu_f32(g)) * u);
+    const float g = T::to_f32(gu[r * 2 * half + c]);
+    const float u = T::to_f32(gu[r * 2 * half + half + c]);
+    h[i] = T::from_f32(T::round(silu_f32(g)) * u);
   }
 }
 
@@ -524,38 +530,60 @@ extern "C" int lm_route_plan(const int64_t *ids, int64_t tokens, int64_t top_k, 
 }
 
 extern "C" int lm_ordered_reduce(const void *v, const int64_t *table, const void *w, int w_dtype,
-                                 void *y, int64_t n, int64_t experts, void *stream) {
+                                 void *y, int64_t n, int64_t experts, int dtype, void *stream) {
   LM_REQUIRE(n > 0 && experts >= 0, LM_EINVAL, "invalid reduce geometry");
-  LM_REQUIRE(w_dtype == LM_BF16 || w_dtype == LM_FP32, LM_EINVAL, "weights must be bf16 or fp32");
+  LM_REQUIRE(w_dtype == LM_BF16 || w_dtype == LM_FP16 || w_dtype == LM_FP32, LM_EINVAL,
+             "weights must be bf16, fp16 or fp32");
+  LM_REQUIRE(dtype == LM_BF16 || dtype == LM_FP16, LM_EINVAL, "values must be bf16 or fp16");
   LM_REQUIRE(v && table && w && y, LM_EINVAL, "null pointer");
-  ordered_reduce_kernel<<<cdiv(n, 256), 256, 0, as_stream(stream)>>>(
-      static_cast<const uint16_t *>(v), table, w, w_dtype, static_cast<uint16_t *>(y), (int)n,
-      (int)experts);
+  const unsigned g = cdiv(n, 256);
+  const uint16_t *vp = static_cast<const uint16_t *>(v);
+  uint16_t *yp = static_cast<uint16_t *>(y);
+  if (dtype == LM_BF16)
+    ordered_reduce_kernel<BF16><<<g, 256, 0, as_stream(stream)>>>(vp, table, w, w_dtype, yp,
+                                                                  (int)n, (int)experts);
+  else
+    ordered_reduce_kernel<FP16><<<g, 256, 0, as_stream(stream)>>>(vp, table, w, w_dtype, yp,
+                                                                  (int)n, (int)experts);
   return check_launch("ordered_reduce_kernel");
 }
 
 extern "C" int lm_routed_reduce(const void *v, const int64_t *ordered, const int64_t *slots,
                                 const void *w, int w_dtype, void *y, int64_t tokens, int64_t n,
-                                int64_t top_k, void *stream) {
+                                int64_t top_k, int dtype, void *stream) {
   LM_REQUIRE(n > 0 && tokens >= 0 && top_k >= 1, LM_EINVAL, "invalid reduce geometry");
-  LM_REQUIRE(w_dtype == LM_BF16 || w_dtype == LM_FP32, LM_EINVAL, "weights must be bf16 or fp32");
+  LM_REQUIRE(w_dtype == LM_BF16 || w_dtype == LM_FP16 || w_dtype == LM_FP32, LM_EINVAL,
+             "weights must be bf16, fp16 or fp32");
+  LM_REQUIRE(dtype == LM_BF16 || dtype == LM_FP16, LM_EINVAL, "values must be bf16 or fp16");
   if (tokens == 0) return LM_OK;
   LM_REQUIRE(tokens < 65536, LM_EINVAL, "too many tokens for one launch");
   LM_REQUIRE(v && ordered && slots && w && y, LM_EINVAL, "null pointer");
-  routed_reduce_kernel<<<dim3(cdiv(n, 256), (unsigned)tokens), 256, 0, as_stream(stream)>>>(
-      static_cast<const uint16_t *>(v), ordered, slots, w, w_dtype, static_cast<uint16_t *>(y),
-      (int)n, (int)top_k);
+  const dim3 grid(cdiv(n, 256), (unsigned)tokens);
+  const uint16_t *vp = static_cast<const uint16_t *>(v);
+  uint16_t *yp = static_cast<uint16_t *>(y);
+  if (dtype == LM_BF16)
+    routed_reduce_kernel<BF16><<<grid, 256, 0, as_stream(stream)>>>(
+        vp, ordered, slots, w, w_dtype, yp, (int)n, (int)top_k, tokens * top_k);
+  else
+    routed_reduce_kernel<FP16><<<grid, 256, 0, as_stream(stream)>>>(
+        vp, ordered, slots, w, w_dtype, yp, (int)n, (int)top_k, tokens * top_k);
   return check_launch("routed_reduce_kernel");
 }
 
-extern "C" int lm_swiglu(const void *gu, void *h, int64_t rows, int64_t half, void *stream) {
+extern "C" int lm_swiglu(const void *gu, void *h, int64_t rows, int64_t half, int dtype,
+                         void *stream) {
   LM_REQUIRE(rows >= 0 && half > 0, LM_EINVAL, "invalid SwiGLU geometry");
+  LM_REQUIRE(dtype == LM_BF16 || dtype == LM_FP16, LM_EINVAL, "SwiGLU input must be bf16 or fp16");
   if (rows == 0) return LM_OK;
   LM_REQUIRE(gu && h, LM_EINVAL, "null pointer");
   int64_t blocks = (rows * half + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  swiglu_kernel<<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
-      static_cast<const uint16_t *>(gu), static_cast<uint16_t *>(h), rows, half);
+  const uint16_t *gp = static_cast<const uint16_t *>(gu);
+  uint16_t *hp = static_cast<uint16_t *>(h);
+  if (dtype == LM_BF16)
+    swiglu_kernel<BF16><<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(gp, hp, rows, half);
+  else
+    swiglu_kernel<FP16><<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(gp, hp, rows, half);
   return check_launch("swiglu_kernel");
 }
 

@@ -30,15 +30,9 @@
 namespace lm {
 namespace {
 
-constexpr int kQBM = 128;        // tile rows
-#ifndef LM_W8A8_BN
-#define LM_W8A8_BN 128
-#endif
-#ifndef LM_W8A8_OCC
-#define LM_W8A8_OCC 2
-#endif
-constexpr int kQBN = LM_W8A8_BN;    // tile columns
-constexpr int kQOcc = LM_W8A8_OCC;  // workgroups per CU the register budget targets
+constexpr int kQBM = 128;  // tile rows
+constexpr int kQBN = 128;  // tile columns
+constexpr int kQOcc = 2;   // workgroups per CU the register budget targets
 constexpr int kQG = 128;         // K group
 constexpr int kQPitch = kQG + 16;  // LDS bytes per staged row
 
@@ -55,7 +49,7 @@ struct W8A8GemmArgs {
   int nt_count, mt_count;
 };
 
-template <bool SWIGLU, int BN, int OCC>
+template <typename T, bool SWIGLU, int BN, int OCC>
 __global__ __launch_bounds__(256, OCC) void w8a8_mfma_kernel(W8A8GemmArgs a) {
   constexpr int MI = 4, NI = BN / 32;  // 16x16 sub-tiles per wave (64 x BN/2)
   constexpr int BCH = BN / 32;         // 16-byte B chunks per thread per group
@@ -214,16 +208,16 @@ __global__ __launch_bounds__(256, OCC) void w8a8_mfma_kernel(W8A8GemmArgs a) {
         for (int ni = 0; ni < NI / 2; ++ni) {
           const int col = n0 + wn * (BN / 4) + ni * 16 + (lane & 15);
           if (col < half) {
-            const float gate = round_bf16(acc[mi][ni][it]);
-            const float up = round_bf16(acc[mi][ni + NI / 2][it]);
-            yrow[col] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
+            const float gate = T::round(acc[mi][ni][it]);
+            const float up = T::round(acc[mi][ni + NI / 2][it]);
+            yrow[col] = T::from_f32(T::round(silu_f32(gate)) * up);
           }
         }
       } else {
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
           const int col = n0 + col_base(ni) + (lane & 15);
-          if (col < a.N) yrow[col] = f32_to_bf16_bits(acc[mi][ni][it]);
+          if (col < a.N) yrow[col] = T::from_f32(acc[mi][ni][it]);
         }
       }
     }
@@ -236,7 +230,10 @@ __global__ __launch_bounds__(256, OCC) void w8a8_mfma_kernel(W8A8GemmArgs a) {
 using namespace lm;
 
 extern "C" int lm_w8a8_gemm(const int8_t *xq, const float *xs, const int8_t *q, const float *s,
-                            void *y, int64_t m, int64_t n, int64_t k, int swiglu, void *stream) {
+                            void *y, int64_t m, int64_t n, int64_t k, int swiglu, int y_dtype,
+                            void *stream) {
+  LM_REQUIRE(y_dtype == LM_BF16 || y_dtype == LM_FP16, LM_EINVAL,
+             "W8A8 output must be bf16 or fp16");
   LM_REQUIRE(m >= 0 && m <= (int64_t(1) << 31) / 128, LM_EINVAL, "invalid row count");
   LM_REQUIRE(n > 0 && n <= (1 << 24) && k > 0 && k % 128 == 0 && k <= 65536, LM_EINVAL,
              "Invalid INT8 group geometry");
@@ -258,9 +255,13 @@ extern "C" int lm_w8a8_gemm(const int8_t *xq, const float *xs, const int8_t *q, 
   const int64_t grid = 8 * (int64_t)a.nt_count * ((a.mt_count + 7) / 8);
   LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
   hipStream_t st = as_stream(stream);
-  if (swiglu)
-    w8a8_mfma_kernel<true, kQBN, kQOcc><<<(unsigned)grid, 256, 0, st>>>(a);
-  else
-    w8a8_mfma_kernel<false, kQBN, kQOcc><<<(unsigned)grid, 256, 0, st>>>(a);
+  const bool bf = y_dtype == LM_BF16;
+  if (swiglu) {
+    if (bf) w8a8_mfma_kernel<BF16, true, kQBN, kQOcc><<<(unsigned)grid, 256, 0, st>>>(a);
+    else w8a8_mfma_kernel<FP16, true, kQBN, kQOcc><<<(unsigned)grid, 256, 0, st>>>(a);
+  } else {
+    if (bf) w8a8_mfma_kernel<BF16, false, kQBN, kQOcc><<<(unsigned)grid, 256, 0, st>>>(a);
+    else w8a8_mfma_kernel<FP16, false, kQBN, kQOcc><<<(unsigned)grid, 256, 0, st>>>(a);
+  }
   return check_launch("w8a8_mfma_kernel");
 }

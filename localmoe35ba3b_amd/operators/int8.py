@@ -64,18 +64,21 @@ def grouped_linear(x, table, experts, n, field, shared):
     table: CUDA int64 [experts, 5] = [gate_up.q, gate_up.s, down.q, down.s, slot]
     data pointers; row e reads x row 0 if shared else row e.
     """
+    if not x.is_cuda or x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError('W8A16 requires CUDA FP16/BF16 activations')
     x = x.contiguous()
     out = torch.empty((experts, n), dtype=x.dtype, device=x.device)
     _lib.call('lm_w8a16_grouped_gemv', x.data_ptr(), table.data_ptr(), out.data_ptr(),
-              experts, n, x.shape[-1], field, int(bool(shared)), _lib.stream(x.device))
+              experts, n, x.shape[-1], field, int(bool(shared)), _lib.dtype_code(x.dtype),
+              _lib.stream(x.device))
     return out
 
 
 def ordered_reduce(values, table, weights, out=None):
-    """Decode combine (int8.py:240-250): acc = bf16(acc + bf16(v_e * w[slot_e])).
+    """Decode combine (int8.py:240-250): acc = T(acc + T(v_e * w[slot_e])).
 
-    values bf16 [E_sel, N] in ascending-expert table order; weights [1, top_k]
-    (bf16 or fp32); returns bf16 [1, N].
+    values [E_sel, N] (bf16 or fp16, T) in ascending-expert table order;
+    weights [1, top_k] (bf16, fp16 or fp32); returns [1, N] in T.
     """
     experts, n = values.shape
     if out is None:
@@ -83,17 +86,17 @@ def ordered_reduce(values, table, weights, out=None):
     weights = weights.contiguous()
     _lib.call('lm_ordered_reduce', values.contiguous().data_ptr(), table.data_ptr(),
               weights.data_ptr(), _lib.dtype_code(weights.dtype), out.data_ptr(), n, experts,
-              _lib.stream(values.device))
+              _lib.dtype_code(values.dtype), _lib.stream(values.device))
     return out
 
 
 def swiglu(gu):
-    """bf16(bf16(silu(gate)) * up) over the two halves of the last dim."""
+    """T(T(silu(gate)) * up) over the two halves of the last dim, T = gu.dtype."""
     gu = gu.contiguous()
     half = gu.shape[-1] // 2
     out = torch.empty((*gu.shape[:-1], half), dtype=gu.dtype, device=gu.device)
     _lib.call('lm_swiglu', gu.data_ptr(), out.data_ptr(), gu.numel() // gu.shape[-1], half,
-              _lib.stream(gu.device))
+              _lib.dtype_code(gu.dtype), _lib.stream(gu.device))
     return out
 
 

@@ -27,3 +27,31 @@ def plan_routes(ids, experts):
     n = int(count.item())
     segments = [tuple(int(v) for v in seg[:, i]) for i in range(n)]
     return positions, segments
+
+
+def tile_plan(ids, experts, bm):
+    """Host route plan in the device plan's format, for CPU routing ids.
+
+    Returns (pos [R], table [n_tiles, 3], ordered [T, k], slots [T, k],
+    active) as int64 CPU tensors: the plan gpu_routes.plan computes on the
+    device, except that the table holds only the bm-row tiles of the
+    non-empty experts (what the reference's host-planned prefill launches,
+    prefill.py:52-68) and `active` counts those experts.  Computed by
+    lm_route_plan_host, one stable counting sort.
+    """
+    if ids.device.type != 'cpu' or ids.ndim != 2 or ids.numel() == 0:
+        raise ValueError('Expected nonempty CPU [tokens,top_k] IDs')
+    flat = ids.to(torch.int64).contiguous()
+    tokens, top = ids.shape
+    routes = flat.numel()
+    capacity = (routes + bm - 1) // bm + int(experts)
+    pos = torch.empty(routes, dtype=torch.int64)
+    table = torch.empty((capacity, 3), dtype=torch.int64)
+    ordered = torch.empty((tokens, top), dtype=torch.int64)
+    slots = torch.empty((tokens, top), dtype=torch.int64)
+    counts = torch.zeros(2, dtype=torch.int64)
+    _lib.call('lm_route_plan_host', flat.data_ptr(), tokens, top, int(experts), int(bm),
+              pos.data_ptr(), table.data_ptr(), capacity, ordered.data_ptr(), slots.data_ptr(),
+              counts[0:1].data_ptr(), counts[1:2].data_ptr())
+    n_tiles, active = (int(v) for v in counts)
+    return pos, table[:n_tiles], ordered, slots, active

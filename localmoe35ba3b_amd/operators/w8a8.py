@@ -32,52 +32,61 @@ def quantize(x):
     return q, s
 
 
-def grouped_linear(x, table, experts, n, field, shared):
-    """Grouped W8A8 decode GEMV; activation quantization is fused into the kernel."""
-    x = x.contiguous()
-    if not x.is_cuda or x.ndim != 2 or x.shape[-1] % 128 or x.dtype != torch.bfloat16:
+def _check_rows(x):
+    if not x.is_cuda or x.ndim != 2 or x.shape[-1] % 128:
         raise ValueError('Expected CUDA rows with K divisible by 128')
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError('Expected CUDA rows with K divisible by 128')
+
+
+def grouped_linear(x, table, experts, n, field, shared):
+    """Grouped W8A8 decode GEMV; activation quantization is fused into the
+    kernel.  x bf16 or fp16; the output is in x.dtype (w8a8.py:46)."""
+    x = x.contiguous()
+    _check_rows(x)
     out = torch.empty((experts, n), device=x.device, dtype=x.dtype)
     _lib.call('lm_w8a8_grouped_linear', x.data_ptr(), table.data_ptr(), out.data_ptr(), experts,
-              n, x.shape[-1], field, int(bool(shared)), _lib.stream(x.device))
+              n, x.shape[-1], field, int(bool(shared)), _lib.dtype_code(x.dtype),
+              _lib.stream(x.device))
     return out
 
 
-def grouped_gemv(q, s, table, experts, n, field, shared):
-    """Grouped W8A8 GEMV on pre-quantized activations (the _linear kernel, w8a8.py:25-41)."""
-    out = torch.empty((experts, n), device=q.device, dtype=torch.bfloat16)
+def grouped_gemv(q, s, table, experts, n, field, shared, out_dtype=torch.bfloat16):
+    """Grouped W8A8 GEMV on pre-quantized activations (the _linear kernel,
+    w8a8.py:25-41); the output in out_dtype (bf16 or fp16)."""
+    out = torch.empty((experts, n), device=q.device, dtype=out_dtype)
     _lib.call('lm_w8a8_grouped_gemv', q.contiguous().data_ptr(), s.contiguous().data_ptr(),
               table.data_ptr(), out.data_ptr(), experts, n, q.shape[-1], field, int(bool(shared)),
-              _lib.stream(q.device))
+              _lib.dtype_code(out_dtype), _lib.stream(q.device))
     return out
 
 
 def linear(x, q, scale, swiglu=False):
-    """Dense W8A8 linear of bf16 rows: bf16 [M, N] or, with swiglu, [M, N/2].
-    Up to 8 rows run as one fused quantize + GEMV launch; more rows are
-    quantized (quantize) and multiplied by the int8 MFMA GEMM (gemm)."""
+    """Dense W8A8 linear of bf16 or fp16 rows: [M, N] or, with swiglu,
+    [M, N/2], in x.dtype.  Up to 8 rows run as one fused quantize + GEMV
+    launch; more rows are quantized (quantize) and multiplied by the int8
+    MFMA GEMM (gemm)."""
     x = x.contiguous()
-    if not x.is_cuda or x.ndim != 2 or x.dtype != torch.bfloat16:
-        raise ValueError('Expected CUDA rows with K divisible by 128')
+    _check_rows(x)
     n, k = q.shape
     if k % 128 or x.shape[-1] != k or tuple(scale.shape) != (n, k // 128):
         raise ValueError('Invalid INT8 group geometry')
     if x.shape[0] > 8:
         xq, xs = quantize(x)
-        return gemm(xq, xs, q, scale, swiglu)
+        return gemm(xq, xs, q, scale, swiglu, out_dtype=x.dtype)
     out = torch.empty((x.shape[0], n // 2 if swiglu else n), device=x.device, dtype=x.dtype)
     _lib.call('lm_w8a8_linear', x.data_ptr(), q.contiguous().data_ptr(),
               scale.contiguous().data_ptr(), out.data_ptr(), x.shape[0], n, k, int(bool(swiglu)),
-              _lib.stream(x.device))
+              _lib.dtype_code(x.dtype), _lib.stream(x.device))
     return out
 
 
-def gemm(xq, xs, q, scale, swiglu=False):
+def gemm(xq, xs, q, scale, swiglu=False, out_dtype=torch.bfloat16):
     """W8A8 GEMM of quantized rows (xq int8 [M, K], xs fp32 [M, K/128], as
     returned by quantize) with int8 weights q [N, K] and fp32 group scales
     [N, K/128]: w8a8._linear (w8a8.py:25-41) for every row, int32 MFMA group
-    partials and the unfused fp32 rescale in ascending group order; bf16
-    [M, N] or, with swiglu, [M, N/2]."""
+    partials and the unfused fp32 rescale in ascending group order; [M, N]
+    or, with swiglu, [M, N/2], in out_dtype (bf16 or fp16)."""
     if not (xq.is_cuda and q.is_cuda) or xq.dtype != torch.int8 or q.dtype != torch.int8:
         raise ValueError('Expected CUDA int8 rows and weights')
     m, k = xq.shape
@@ -87,10 +96,10 @@ def gemm(xq, xs, q, scale, swiglu=False):
         raise ValueError('Invalid INT8 group geometry')
     if swiglu and n % 2:
         raise ValueError('SwiGLU needs an even number of weight rows')
-    out = torch.empty((m, n // 2 if swiglu else n), device=xq.device, dtype=torch.bfloat16)
+    out = torch.empty((m, n // 2 if swiglu else n), device=xq.device, dtype=out_dtype)
     _lib.call('lm_w8a8_gemm', xq.contiguous().data_ptr(), xs.contiguous().data_ptr(),
               q.contiguous().data_ptr(), scale.contiguous().data_ptr(), out.data_ptr(), m, n, k,
-              int(bool(swiglu)), _lib.stream(xq.device))
+              int(bool(swiglu)), _lib.dtype_code(out_dtype), _lib.stream(xq.device))
     return out
 
 

@@ -61,49 +61,76 @@ def _check_bank(q, s):
         raise ValueError('Invalid INT8 group geometry')
 
 
+def _check_activation(x):
+    if not x.is_cuda or x.dtype not in (torch.bfloat16, torch.float16) or x.ndim != 2:
+        raise ValueError('W8A16 requires CUDA FP16/BF16 activations')
+
+
 def routed_gemm(x, q, s, pos, table, bm, gather):
-    """Routed grouped W8A16 GEMM (prefill._routed / _nonempty) -> bf16 [R, N]."""
+    """Routed grouped W8A16 GEMM (prefill._routed / _nonempty) -> [R, N] in x.dtype.
+
+    R = pos.numel(): the rows of the plan; gather reads x[pos[r]], otherwise
+    x[r] (then x needs at least R rows)."""
     _check_bank(q, s)
+    _check_activation(x)
+    x = x.contiguous()
     routes = pos.numel()
     out = torch.empty((routes, q.shape[1]), device=x.device, dtype=x.dtype)
-    _lib.call('lm_routed_gemm_w8a16', x.data_ptr(), q.data_ptr(), s.data_ptr(), pos.data_ptr(),
-              table.data_ptr(), table.shape[0], int(bm), out.data_ptr(), q.shape[1], q.shape[2],
-              int(bool(gather)), q.stride(0), s.stride(0), _lib.stream(x.device))
+    _lib.call('lm_routed_gemm_w8a16', x.data_ptr(), x.shape[0], q.data_ptr(), s.data_ptr(),
+              q.shape[0], q.stride(0), s.stride(0), pos.data_ptr(), table.data_ptr(),
+              table.shape[0], int(bm), out.data_ptr(), routes, q.shape[1], q.shape[2],
+              int(bool(gather)), _lib.dtype_code(x.dtype), _lib.stream(x.device))
     return out
 
 
 def routed_reduce(values, ordered, slots, weights, tokens, n):
-    """Prefill combine (prefill._reduce): ascending-expert bf16 accumulation per token."""
+    """Prefill combine (prefill._reduce): ascending-expert accumulation per
+    token, rounded to the values' dtype at every step."""
     out = torch.empty((tokens, n), device=values.device, dtype=values.dtype)
     weights = weights.contiguous()
     _lib.call('lm_routed_reduce', values.data_ptr(), ordered.data_ptr(), slots.data_ptr(),
               weights.data_ptr(), _lib.dtype_code(weights.dtype), out.data_ptr(), tokens, n,
-              ordered.shape[1], _lib.stream(values.device))
+              ordered.shape[1], _lib.dtype_code(values.dtype), _lib.stream(values.device))
     return out
 
 
-def routed_moe(x, weights, ids, banks, large_tile=False, ready_event=None):
-    """Routed experts of one MoE layer for a prefill chunk -> bf16 [T, H]."""
-    if not x.is_cuda or x.dtype != torch.bfloat16 or x.ndim != 2:
-        raise ValueError('W8A16 requires CUDA FP16/BF16 activations')
-    x = x.contiguous()
-    bm = BM_LARGE if large_tile else BM_DEFAULT
+def run_plan(x, weights, banks, pos, table, ordered, slots, bm, ready_event=None):
+    """The device half of routed_moe for a plan already on the device:
+    grouped gate_up with the SwiGLU glue fused into its epilogue, grouped
+    down, ordered combine (prefill.py:69-85, gpu_routes.py:69-82)."""
+    qg, sg, qd, sd = banks
+    routes = pos.numel()
+    if ready_event is not None:
+        torch.cuda.current_stream().wait_event(ready_event)
+    st = _lib.stream(x.device)
+    code = _lib.dtype_code(x.dtype)
+    hidden = torch.empty((routes, qg.shape[1] // 2), device=x.device, dtype=x.dtype)
+    _lib.call('lm_routed_gate_up_swiglu', x.data_ptr(), x.shape[0], qg.data_ptr(), sg.data_ptr(),
+              qg.shape[0], qg.stride(0), sg.stride(0), pos.data_ptr(), table.data_ptr(),
+              table.shape[0], bm, hidden.data_ptr(), routes, qg.shape[1], qg.shape[2], code, st)
+    down = torch.empty((routes, qd.shape[1]), device=x.device, dtype=x.dtype)
+    _lib.call('lm_routed_gemm_w8a16', hidden.data_ptr(), routes, qd.data_ptr(), sd.data_ptr(),
+              qd.shape[0], qd.stride(0), sd.stride(0), pos.data_ptr(), table.data_ptr(),
+              table.shape[0], bm, down.data_ptr(), routes, qd.shape[1], qd.shape[2], 0, code, st)
+    return routed_reduce(down, ordered, slots, weights, x.shape[0], x.shape[1])
+
+
+def check_banks(x, banks):
+    """Validates x against the routed banks [qg, sg, qd, sd] (reference format)."""
+    _check_activation(x)
     qg, sg, qd, sd = banks
     _check_bank(qg, sg)
     _check_bank(qd, sd)
     if qg.shape[2] != x.shape[1] or qd.shape[2] * 2 != qg.shape[1] or qd.shape[1] != x.shape[1]:
         raise ValueError('Invalid INT8 group geometry')
-    pos, table, ordered, slots = plan(ids, qg.shape[0], bm)
-    routes = ids.numel()
-    if ready_event is not None:
-        torch.cuda.current_stream().wait_event(ready_event)
-    hidden = torch.empty((routes, qg.shape[1] // 2), device=x.device, dtype=x.dtype)
-    st = _lib.stream(x.device)
-    _lib.call('lm_routed_gate_up_swiglu', x.data_ptr(), qg.data_ptr(), sg.data_ptr(),
-              pos.data_ptr(), table.data_ptr(), table.shape[0], bm, hidden.data_ptr(),
-              qg.shape[1], qg.shape[2], qg.stride(0), sg.stride(0), st)
-    down = torch.empty((routes, qd.shape[1]), device=x.device, dtype=x.dtype)
-    _lib.call('lm_routed_gemm_w8a16', hidden.data_ptr(), qd.data_ptr(), sd.data_ptr(),
-              pos.data_ptr(), table.data_ptr(), table.shape[0], bm, down.data_ptr(), qd.shape[1],
-              qd.shape[2], 0, qd.stride(0), sd.stride(0), st)
-    return routed_reduce(down, ordered, slots, weights, x.shape[0], x.shape[1])
+    if qd.shape[0] != qg.shape[0]:
+        raise ValueError('Invalid INT8 group geometry')
+
+
+def routed_moe(x, weights, ids, banks, large_tile=False, ready_event=None):
+    """Routed experts of one MoE layer for a prefill chunk -> [T, H] in x.dtype."""
+    check_banks(x, banks)
+    x = x.contiguous()
+    bm = BM_LARGE if large_tile else BM_DEFAULT
+    pos, table, ordered, slots = plan(ids, banks[0].shape[0], bm)
+    return run_plan(x, weights, banks, pos, table, ordered, slots, bm, ready_event)

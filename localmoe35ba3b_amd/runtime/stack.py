@@ -141,6 +141,26 @@ class MoEStack:
                   _lib.ptr(ids_out), _lib.ptr(weights_out), ev, _lib.stream(h.device))
         return h
 
+    _REGION_TYPES = {'normed': (torch.bfloat16, 'H'), 'gate': (torch.float32, None),
+                     'ids': (torch.int64, 'K'), 'weights': (torch.bfloat16, 'K'),
+                     'route_rows': (torch.int32, 'K'), 'hidden': (torch.bfloat16, 'I'),
+                     'down': (torch.bfloat16, 'H')}
+
+    def workspace_view(self, region, tokens, workspace=None):
+        """Typed view of one intermediate a prefill call on `tokens` rows left
+        in the workspace (lm_moe_workspace_region): 'normed', 'gate', 'ids',
+        'weights', 'route_rows', 'hidden' or 'down'.  Valid until the next
+        call that uses the same workspace."""
+        ws = self.workspace if workspace is None else workspace
+        off, nbytes = ctypes.c_int64(), ctypes.c_int64()
+        _lib.call('lm_moe_workspace_region', tokens, _lib.WS_REGIONS[region],
+                  ctypes.byref(off), ctypes.byref(nbytes))
+        dtype, inner = self._REGION_TYPES[region]
+        raw = ws[off.value:off.value + nbytes.value].view(dtype)
+        if inner is None:
+            return raw
+        return raw.view(-1, {'H': self.H, 'I': self.I, 'K': self.K}[inner])
+
     def forward(self, h, layers=None):
         for l in range(self.L if layers is None else layers):
             self.layer_forward(h, l)

@@ -23,13 +23,25 @@ GROUP = 128
 
 # ----------------------------------------------------------------- rounding
 def bf16(a):
-    """Round-to-nearest-even to bf16, returned as float32 (bit manipulation)."""
+    """Round-to-nearest-even to bf16, returned as float32 (bit manipulation):
+    add 0x7FFF plus the lowest kept bit, clear the low 16 bits.  In uint32
+    arithmetic the sum wraps only for bit patterns >= 0xFFFF8000, which are
+    NaNs and are replaced by NaN."""
     a = np.ascontiguousarray(a, dtype=np.float32)
-    b = a.view(np.uint32).astype(np.uint64)
-    rounded = (b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000
+    b = a.view(np.uint32)
+    rounded = (b + np.uint32(0x7FFF) + ((b >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    out = rounded.view(np.float32)
     nan = np.isnan(a)
-    out = rounded.astype(np.uint32).view(np.float32)
-    return np.where(nan, np.float32(np.nan), out).astype(np.float32)
+    if nan.any():
+        out = np.where(nan, np.float32(np.nan), out).astype(np.float32)
+    return out
+
+
+def fp16(a):
+    """Round-to-nearest-even to fp16 (numpy's float16 conversion), returned as
+    float32.  The reference runs an fp16 model with every rounding step of
+    the bf16 path in fp16 instead (outputs are allocated in x.dtype)."""
+    return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float32)
 
 
 def to_torch_bf16(a):
@@ -102,18 +114,24 @@ def w8a8_accumulate(p, xs, ws):
     return acc
 
 
-def w8a8_linear(x, wq, ws):
-    """w8a8.grouped_linear for one weight matrix (w8a8.py:44-48): bf16 out [M, N]."""
+def w8a8_linear(x, wq, ws, round_to=bf16):
+    """w8a8.grouped_linear for one weight matrix (w8a8.py:44-48): [M, N] in
+    x.dtype T (bf16 or fp16)."""
     xq, xs = act_quant(x)
-    return bf16(w8a8_accumulate(w8a8_partials(xq, wq), xs, ws))
+    return round_to(w8a8_accumulate(w8a8_partials(xq, wq), xs, ws))
 
 
 # ----------------------------------------------------------------- a2 W8A16
-def w8a16_linear(x, q, s):
-    """int8.linear (int8.py:9-37): bf16(x . bf16(q*s)^T), fp32 accumulation (torch CPU)."""
-    xt = to_torch_bf16(x)
-    wt = to_torch_bf16(dequant(q, s))
-    return from_torch(F.linear(xt, wt))
+def w8a16_linear(x, q, s, round_to=bf16):
+    """int8.linear (int8.py:9-37): T(x . T(q*s)^T) with fp32 accumulation, T =
+    bf16 (torch-CPU bf16 F.linear) or fp16 (round_to=fp16: the products of
+    the fp16 operands summed in float64, then rounded to fp16)."""
+    if round_to is bf16:
+        xt = to_torch_bf16(x)
+        wt = to_torch_bf16(dequant(q, s))
+        return from_torch(F.linear(xt, wt))
+    w = dequant(q, s, round_to).astype(np.float64)
+    return round_to((round_to(x).astype(np.float64) @ w.T).astype(np.float32))
 
 
 # ----------------------------------------------------------------- a11 SwiGLU
@@ -122,23 +140,24 @@ def silu_f32(g):
     return (g / (np.float32(1) + np.exp(-g))).astype(np.float32)
 
 
-def swiglu(gu):
-    """`gate, up = gu.chunk(2, -1); silu(gate) * up` on bf16 (HF:715, prefill.py:77-78):
-    h = bf16(bf16(silu(gate)) * up)."""
+def swiglu(gu, round_to=bf16):
+    """`gate, up = gu.chunk(2, -1); silu(gate) * up` on T (HF:715, prefill.py:77-78):
+    h = T(T(silu(gate)) * up), T = bf16 or fp16."""
     gu = np.asarray(gu, np.float32)
     half = gu.shape[-1] // 2
     gate, up = gu[..., :half], gu[..., half:]
-    return bf16(bf16(silu_f32(gate)) * up)
+    return round_to(round_to(silu_f32(gate)) * up)
 
 
 # ----------------------------------------------------------------- a6 / a12 combine
-def ordered_combine(values, weights):
+def ordered_combine(values, weights, round_to=bf16):
     """int8._ordered_reduce / prefill._reduce (int8.py:240-250, prefill.py:37-49):
-    over rows in the given (ascending expert) order acc = bf16(acc + bf16(v * w))."""
+    over rows in the given (ascending expert) order acc = T(acc + T(v * w)),
+    T = bf16 or fp16 (the output dtype)."""
     values = np.asarray(values, np.float32)
     acc = np.zeros(values.shape[1:], dtype=np.float32)
     for v, w in zip(values, np.asarray(weights, np.float32)):
-        acc = bf16(acc + bf16(v * np.float32(w)))
+        acc = round_to(acc + round_to(v * np.float32(w)))
     return acc
 
 
@@ -262,14 +281,16 @@ def rmsnorm(x, w=None, eps=1e-6):
     return bf16(y).reshape(shape)
 
 
-def expert_w8a16(x, gu_q, gu_s, dn_q, dn_s):
-    """One expert MLP in W8A16 (int8.linear twice + SwiGLU), bf16 [M, H]."""
-    return w8a16_linear(swiglu(w8a16_linear(x, gu_q, gu_s)), dn_q, dn_s)
+def expert_w8a16(x, gu_q, gu_s, dn_q, dn_s, round_to=bf16):
+    """One expert MLP in W8A16 (int8.linear twice + SwiGLU), [M, H] in T."""
+    h = swiglu(w8a16_linear(x, gu_q, gu_s, round_to), round_to)
+    return w8a16_linear(h, dn_q, dn_s, round_to)
 
 
-def expert_w8a8(x, gu_q, gu_s, dn_q, dn_s):
-    """One expert MLP in W8A8 (w8a8.grouped_linear twice + SwiGLU), bf16 [M, H]."""
-    return w8a8_linear(swiglu(w8a8_linear(x, gu_q, gu_s)), dn_q, dn_s)
+def expert_w8a8(x, gu_q, gu_s, dn_q, dn_s, round_to=bf16):
+    """One expert MLP in W8A8 (w8a8.grouped_linear twice + SwiGLU), [M, H] in T."""
+    h = swiglu(w8a8_linear(x, gu_q, gu_s, round_to), round_to)
+    return w8a8_linear(h, dn_q, dn_s, round_to)
 
 
 def moe_block(x, layer, k=8, w8a8_routed=None, routing=None):

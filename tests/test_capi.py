@@ -46,23 +46,42 @@ def test_invalid_geometry_rejected_before_launch():
     assert b'K divisible by 128' in lib.lm_last_error()
     assert lib.lm_route_plan(None, 4, 8, 300, 16, None, None, 0, None, None, None) == _lib.LM_EINVAL
     assert lib.lm_route_plan(None, 4, 8, 256, 16, None, None, 5, None, None, None) == _lib.LM_EINVAL
-    assert lib.lm_routed_gemm_w8a16(None, None, None, None, None, 1, 200, None, 64, 128, 1, 0, 0,
-                                    None) == _lib.LM_EINVAL
+    # tile height beyond 128, then an fp32 activation type
+    assert lib.lm_routed_gemm_w8a16(None, 1, None, None, 256, 0, 0, None, None, 1, 200, None, 16,
+                                    64, 128, 1, 0, None) == _lib.LM_EINVAL
+    assert lib.lm_routed_gemm_w8a16(None, 1, None, None, 256, 0, 0, None, None, 1, 96, None, 16,
+                                    64, 128, 1, 2, None) == _lib.LM_EINVAL
+    assert b'FP16/BF16' in lib.lm_last_error()
+    # contiguous rows need at least as many activation rows as output rows
+    fake = ctypes.c_void_p(256)
+    assert lib.lm_routed_gemm_w8a16(fake, 8, fake, fake, 256, 0, 0, None, fake, 1, 96, fake, 16,
+                                    64, 128, 0, 0, None) == _lib.LM_EINVAL
+    assert b'more output rows' in lib.lm_last_error()
+    assert lib.lm_routed_gate_up_swiglu(fake, 8, fake, fake, 256, 0, 0, None, fake, 1, 96, fake,
+                                        16, 64, 128, 0, None) == _lib.LM_EINVAL
+    assert b'gather needs pos' in lib.lm_last_error()
     assert lib.lm_router_topk(None, None, None, None, None, None, 1, 512, 2048, 8,
                               None) == _lib.LM_EINVAL
-    assert lib.lm_w8a8_linear(None, None, None, None, 9, 64, 128, 0, None) == _lib.LM_EINVAL
-    assert lib.lm_w8a8_gemm(None, None, None, None, None, 9, 64, 100, 0, None) == _lib.LM_EINVAL
+    assert lib.lm_w8a8_linear(None, None, None, None, 9, 64, 128, 0, 0, None) == _lib.LM_EINVAL
+    assert lib.lm_w8a8_linear(None, None, None, None, 1, 64, 128, 0, 2, None) == _lib.LM_EINVAL
+    assert lib.lm_w8a8_gemm(None, None, None, None, None, 9, 64, 100, 0, 0, None) == _lib.LM_EINVAL
     assert b'Invalid INT8 group geometry' in lib.lm_last_error()
-    assert lib.lm_w8a8_gemm(None, None, None, None, None, 9, 63, 128, 1, None) == _lib.LM_EINVAL
-    assert lib.lm_w8a8_gemm(None, None, None, None, None, 9, 64, 128, 0, None) == _lib.LM_EINVAL
+    assert lib.lm_w8a8_gemm(None, None, None, None, None, 9, 63, 128, 1, 0, None) == _lib.LM_EINVAL
+    assert lib.lm_w8a8_gemm(None, None, None, None, None, 9, 64, 128, 0, 0, None) == _lib.LM_EINVAL
     assert b'null pointer' in lib.lm_last_error()
-    assert lib.lm_w8a8_gemm(None, None, None, None, None, 0, 64, 128, 0, None) == _lib.LM_OK
+    assert lib.lm_w8a8_gemm(None, None, None, None, None, 9, 64, 128, 0, 2, None) == _lib.LM_EINVAL
+    assert b'bf16 or fp16' in lib.lm_last_error()
+    assert lib.lm_w8a8_gemm(None, None, None, None, None, 0, 64, 128, 0, 0, None) == _lib.LM_OK
     # a grid beyond one launch is refused before anything is launched (the
     # non-null placeholder pointers are never dereferenced)
-    fake = ctypes.c_void_p(256)
-    assert lib.lm_w8a8_gemm(fake, fake, fake, fake, fake, 1 << 24, 1 << 24, 128, 0,
+    assert lib.lm_w8a8_gemm(fake, fake, fake, fake, fake, 1 << 24, 1 << 24, 128, 0, 0,
                             None) == _lib.LM_EINVAL
     assert b'too large' in lib.lm_last_error()
+    assert lib.lm_swiglu(fake, fake, 4, 64, 2, None) == _lib.LM_EINVAL
+    assert lib.lm_ordered_reduce(fake, fake, fake, 0, fake, 64, 8, 2, None) == _lib.LM_EINVAL
+    assert lib.lm_routed_reduce(fake, fake, fake, fake, 3, fake, 4, 64, 8, 0,
+                                None) == _lib.LM_EINVAL
+    assert lib.lm_moe_workspace_init(fake, 258, None) == _lib.LM_EINVAL
 
 
 def test_moe_layer_bounds_rejected_before_launch():
@@ -126,3 +145,36 @@ def test_host_plan_routes_matches_oracle(t, k, e):
     ref_pos, ref_seg = O.plan_routes(ids, e)
     assert np.array_equal(positions.numpy(), ref_pos)
     assert segments == ref_seg
+
+
+@pytest.mark.parametrize('t,k,e,bm', [(1, 8, 256, 96), (13, 8, 256, 16), (2048, 8, 256, 96),
+                                      (5, 3, 7, 2), (300, 8, 256, 128)])
+def test_host_tile_plan_matches_oracle(t, k, e, bm):
+    """The native host planner (lm_route_plan_host) behind runtime/prefill.py
+    gives the oracle's pos / ordered / slots bit for bit and its tile table
+    without the surplus rows."""
+    rng = np.random.default_rng(7 * t + e)
+    ids = np.stack([rng.choice(e, size=k, replace=False) for _ in range(t)]).astype(np.int64)
+    if t == 300:  # skewed: most routes on a few experts, most experts empty
+        ids = np.stack([rng.choice(12, size=k, replace=False) * 3 for _ in range(t)])
+    pos, table, ordered, slots, active = routing.tile_plan(torch.from_numpy(ids), e, bm)
+    rpos, rtable, rordered, rslots = O.plan(ids, e, bm)
+    assert np.array_equal(pos.numpy(), rpos)
+    assert np.array_equal(ordered.numpy(), rordered)
+    assert np.array_equal(slots.numpy(), rslots)
+    n = table.shape[0]
+    assert np.array_equal(table.numpy(), rtable[:n])
+    assert not rtable[n:].any()  # the oracle's remaining rows are surplus (0, 0, 0)
+    assert active == len(np.unique(ids))
+
+
+def test_host_tile_plan_duplicate_ids_and_errors():
+    ids = torch.tensor([[3, 3, 1], [0, 3, 3]])  # duplicates inside a token: stable order
+    pos, table, ordered, slots, _ = routing.tile_plan(ids, 4, 2)
+    rpos, rtable, rordered, rslots = O.plan(ids.numpy(), 4, 2)
+    assert np.array_equal(slots.numpy(), rslots) and np.array_equal(ordered.numpy(), rordered)
+    assert np.array_equal(pos.numpy(), rpos)
+    with pytest.raises(ValueError, match='Out-of-range expert ID'):
+        routing.tile_plan(torch.tensor([[0, 4]]), 4, 2)
+    with pytest.raises(ValueError, match='Expected nonempty CPU'):
+        routing.tile_plan(torch.zeros(0, 2, dtype=torch.int64), 4, 2)

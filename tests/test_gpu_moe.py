@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 import torch
 
+from localmoe35ba3b_amd import router
 from localmoe35ba3b_amd.runtime.stack import EPS, SyntheticMoEStack, zipf_bias
 from oracle import moe_oracle as O
 from tests.conftest import BF16_TOL, assert_close
@@ -252,3 +253,58 @@ def test_prefill_router_boundary(dev, mode):
     assert np.abs(npf(wts) - rw).max() <= 2.0 ** -8
     if mode == 'all_equal':
         assert (ids.cpu().numpy() == np.arange(8)).all()
+
+
+def test_fused_prefill_combine_bit_exact(dev):
+    """The fused prefill combine (prefill_combine_kernel) on the exact bf16
+    inputs it consumed: the down rows, routing weights and route rows the
+    call left in its workspace.  Per token, routes in ascending expert id,
+    acc = bf16(acc + bf16(v * w)) (prefill.py:37-49), then the gated shared
+    expert and the residual, bit for bit.  The shared gate weight is zero, so
+    its sigmoid is exactly 0.5 and no transcendental enters the check."""
+    st = SyntheticMoEStack(layers=1, seed=51, device=dev, max_tokens=2048)
+    st.gate_w.zero_()
+    h = inputs(2048, 52, dev)
+    out, ids, wts = run_layer(st, h)
+    T, R = 2048, 2048 * 8
+    v = npf(st.workspace_view('down', T))
+    rows = st.workspace_view('route_rows', T).cpu().numpy()
+    gate = st.workspace_view('gate', T).cpu().numpy()
+    assert (gate == 0).all()
+    assert torch.equal(st.workspace_view('ids', T).to(torch.int32), ids)
+    assert torch.equal(st.workspace_view('weights', T), wts)
+    idn, wn, hn = ids.cpu().numpy(), npf(wts), npf(h)
+    # every route has its own row; the routed rows are a permutation of [0, R)
+    assert np.array_equal(np.sort(rows.reshape(-1)), np.arange(R))
+    for tok in range(T):
+        order = np.argsort(idn[tok], kind='stable')
+        routed = O.ordered_combine(v[rows[tok, order]], wn[tok, order])
+        block = O.bf16(routed + O.bf16(np.float32(0.5) * v[R + tok]))
+        assert np.array_equal(npf(out[tok]), O.bf16(hn[tok] + block)), tok
+
+
+def test_prefill_weights_vs_exact_router(dev, capsys):
+    """The fused prefill router selects with exact logits only for the
+    experts its error bound leaves open; the softmax denominator sees the
+    rounded approximate logits of the others.  On the same normalized rows,
+    its ids equal the all-exact router's (lm_router_topk) bit for bit and its
+    weights differ by at most one bf16 step; the mismatch rate is reported."""
+    st = SyntheticMoEStack(layers=2, seed=53, device=dev, max_tokens=2048)
+    total = mismatched = 0
+    for l, seed in ((0, 54), (1, 55), (0, 56)):
+        h = inputs(2048, seed, dev)
+        _, ids, wts = run_layer(st, h, l)
+        xn = st.workspace_view('normed', 2048).clone()
+        assert torch.equal(xn, router.rmsnorm(h, None, EPS))
+        _, ewts, eids = router.router_topk(xn, st.router_w[l], 8)
+        assert torch.equal(ids.to(torch.int64), eids)
+        a = wts.view(torch.int16).to(torch.int32)
+        b = ewts.view(torch.int16).to(torch.int32)
+        assert (a - b).abs().max().item() <= 1  # same sign: one bit step = one bf16 ulp
+        total += a.numel()
+        mismatched += int((a != b).sum())
+    rate = mismatched / total
+    with capsys.disabled():
+        print(f'\n[prefill router] weights differing from the all-exact router: '
+              f'{mismatched} of {total} ({rate:.2e})')
+    assert rate < 1e-2

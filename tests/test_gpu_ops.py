@@ -379,3 +379,57 @@ def test_plan_routes_host_matches_device(dev):
     assert torch.equal(positions[0], pos.cpu())
     tiles = [(e, s0, stop) for e, b, stop in segments for s0 in range(b, stop, 16)]
     assert [tuple(r) for r in table[:len(tiles)].cpu().tolist()] == tiles
+
+
+# ------------------------------------------------------------- a12 bit-exact, f4 lm_head
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
+def test_routed_reduce_bit_exact(dev, dtype):
+    """Prefill combine (prefill._reduce, prefill.py:37-49) on identical inputs:
+    per token, its routes in ascending expert id, acc = T(acc + T(v * w)),
+    bit for bit against the oracle's ordered_combine, including a token whose
+    weights arrive in fp32."""
+    rnd = O.bf16 if dtype == torch.bfloat16 else O.fp16
+    t, k, e, n = 300, 8, 256, 2048
+    ids = _ids(seeded(50), t, e, k, True)
+    pos, table, ordered, slots = gpu_routes.plan(ids.to(dev), e, 96)
+    gen = seeded(51)
+    v = (torch.randn(t * k, n, generator=gen) * 2).to(dtype)
+    w = torch.softmax(torch.randn(t, k, generator=gen), -1).to(dtype)
+    y = gpu_routes.routed_reduce(v.to(dev), ordered, slots, w.to(dev), t, n)
+    vn, wn, idn = v.float().numpy(), w.float().numpy(), ids.numpy()
+    rpos, _, rordered, rslots = O.plan(idn, e, 96)
+    for tok in range(t):
+        rows = vn[rordered[tok]]                     # its routes' rows, ascending expert
+        wts = wn[tok, rslots[tok]]
+        assert np.array_equal(y[tok].float().cpu().numpy(), O.ordered_combine(rows, wts, rnd))
+    y32 = gpu_routes.routed_reduce(v.to(dev), ordered, slots, w.float().to(dev), t, n)
+    assert torch.equal(y32, y)
+
+
+LM_HEAD_N = 248320  # vocabulary of the 35B-A3B configuration
+
+
+@pytest.mark.parametrize('m', [1, 2])
+def test_lm_head_vocab_shape(dev, m):
+    """int8.linear at the lm_head shape, [m, 2048] x [248320, 2048] (the
+    reference quantizes lm_head with the same rule, convert.py:80-81, and runs
+    it through int8.linear, int8.py:26-37): a sample of output rows spread over
+    the whole vocabulary, always including the first and last rows, against
+    the oracle; every row is finite and rows of the sample's neighbours
+    agree with an integer-exact reconstruction."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(60)
+    w = torch.randn((LM_HEAD_N, 2048), generator=gen, device=dev) * 0.02
+    q, s = convert.quantize_g128(w)
+    del w
+    x = torch.randn((m, 2048), generator=gen, device=dev).to(torch.bfloat16)
+    y = int8.linear(x, q, s)
+    torch.cuda.synchronize()
+    assert y.shape == (m, LM_HEAD_N) and torch.isfinite(y.float()).all()
+    rows = np.unique(np.concatenate([
+        np.random.default_rng(61).choice(LM_HEAD_N, 250, replace=False),
+        np.arange(16), np.arange(LM_HEAD_N - 16, LM_HEAD_N)]))
+    idx = torch.from_numpy(rows).to(dev)
+    qs, ss = q[idx].cpu().numpy(), s[idx].cpu().numpy()
+    ref = O.w8a16_linear(npf(x), qs, ss)
+    assert_close(npf(y)[:, rows], ref, BF16_TOL, f'lm_head m={m}')

@@ -14,6 +14,8 @@ Sources of truth, per function:
   plan/plan_routes pure-Python definitions on ragged inputs with empty experts
   rmsnorm          float64 formula
   moe_block        float64 dense formulation of the whole block
+  fp16 variants    exact-rational fp16 rounding with ties; torch's independent fp16
+                   cast; the fp16 GEMM/SwiGLU/combine against float64 and scalar loops
 """
 import math
 from fractions import Fraction
@@ -373,3 +375,62 @@ def test_moe_block_vs_float64_dense(tokens):
     # the bf16 rounding chain; 5e-2 norm-wise covers both
     rel = np.linalg.norm(out - ref) / np.linalg.norm(ref)
     assert rel < 5e-2
+
+
+# ------------------------------------------------------------- fp16 activations
+def round_f16(fr):
+    """Round a Fraction to the nearest fp16 value (ties to even), exactly;
+    normal range only."""
+    fr = Fraction(fr)
+    if fr == 0:
+        return 0.0
+    sign = -1 if fr < 0 else 1
+    a = abs(fr)
+    e = math.floor(math.log2(a.numerator) - math.log2(a.denominator))
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    ulp = Fraction(2) ** (e - 10)
+    m = a / ulp
+    lo = math.floor(m)
+    rem = m - lo
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and lo % 2 == 1):
+        lo += 1
+    return sign * float(lo * ulp)
+
+
+def test_fp16_rounding_exact_rational_and_torch():
+    rng = np.random.default_rng(40)
+    v = (rng.standard_normal(2000) * 30).astype(np.float32)
+    ties = np.array([1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, -(2 + 2.0 ** -10)], np.float32)
+    v = np.concatenate([v, ties])
+    got = O.fp16(v)
+    for i in list(range(0, 2000, 37)) + [2000, 2001, 2002]:
+        assert got[i] == np.float32(round_f16(Fraction(float(v[i])))), v[i]
+    assert np.array_equal(got, torch.from_numpy(v).half().float().numpy())
+    assert got[2000] == 1.0 and got[2001] == np.float32(1 + 2.0 ** -9)  # ties to even
+
+
+def test_fp16_paths_vs_float64_and_scalar_loops():
+    rng = np.random.default_rng(41)
+    x = O.fp16(rng.standard_normal((5, 256)).astype(np.float32))
+    q, s = O.quantize_weight((rng.standard_normal((64, 256)) * 0.02).astype(np.float32))
+    y = O.w8a16_linear(x, q, s, O.fp16)
+    ref = x.astype(np.float64) @ (q.astype(np.float64).reshape(64, 2, 128)
+                                  * s[..., None]).reshape(64, 256).T
+    assert_close(y, ref, 1e-2, 'w8a16 fp16 vs f64')
+    assert np.array_equal(y, O.fp16(y))  # outputs are fp16 values
+    gu = O.fp16(rng.standard_normal((4, 64)).astype(np.float32) * 3)
+    h = O.swiglu(gu, O.fp16)
+    g, u = gu[:, :32].astype(np.float64), gu[:, 32:].astype(np.float64)
+    assert_close(h, g / (1 + np.exp(-g)) * u, 1e-2, 'swiglu fp16')
+    v = O.fp16(rng.standard_normal((8, 16)).astype(np.float32))
+    w = O.fp16(rng.random(8).astype(np.float32))
+    out = O.ordered_combine(v, w, O.fp16)
+    for n in range(16):
+        acc = torch.tensor(0.0, dtype=torch.float16)
+        for e in range(8):
+            term = (torch.tensor(float(v[e, n])) * torch.tensor(float(w[e]))).half()
+            acc = (acc.float() + term.float()).half()
+        assert out[n] == np.float32(acc.item())
