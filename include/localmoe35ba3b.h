@@ -305,6 +305,23 @@ int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t tokens,
                          void *weights_out, void *const *phase_events,
                          void *stream);
 
+/* lm_moe_layer_forward without a workspace argument: the call's workspace
+ * is a device array inside the library (one per device, about 6.6 MB, held
+ * until the process ends), so the call allocates nothing and takes no
+ * scratch from the caller.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory - code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  At most
+ * lm_moe_static_max_tokens() (128) tokens per call (LM_ENOMEM beyond);
+ * same results as lm_moe_layer_forward.  Every call on one device shares
+ * that device's array: calls that overlap on a device (several streams or
+ * host threads) race and must be serialized by the caller. */
+int64_t lm_moe_static_max_tokens(void);
+int lm_moe_layer_forward_static(const lm_moe_layer *layer, void *h,
+                                int64_t tokens, int64_t hidden, int64_t inter,
+                                int64_t experts, int64_t top_k, float eps,
+                                int32_t *ids_out, void *weights_out,
+                                void *const *phase_events, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

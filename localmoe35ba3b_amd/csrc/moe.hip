@@ -19,6 +19,7 @@
 // appended as extra tiles), grouped W8A16 gate_up GEMM with fused SwiGLU,
 // grouped W8A16 down GEMM, and a per-token combine.
 #include <algorithm>
+#include <mutex>
 
 #include "gemv_core.hpp"
 #include "internal.hpp"
@@ -39,9 +40,9 @@ struct WsLayout {
   int64_t max_tiles, n_tiles;
 };
 
-static int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
+constexpr int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
-static WsLayout layout(int64_t T) {
+constexpr WsLayout layout(int64_t T) {
   WsLayout w{};
   const int64_t R = T * kTopK;
   w.max_tiles = (R + kBM - 1) / kBM + kE;
@@ -1009,6 +1010,44 @@ extern "C" int lm_moe_workspace_init(void *workspace, int64_t bytes, void *strea
   return check_launch("fill_zero_kernel");
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free variant: the workspace of calls up to kScratchMaxTokens
+// tokens lives in a file-scope device array.  Each device that runs the
+// library holds its own copy until the process ends; its address on a
+// device comes from hipGetSymbolAddress, taken once per device (with that
+// device current) on the first call there and kept.  Every call on a device
+// shares that device's array, so calls that overlap on one device (other
+// streams, other host threads) race.  No region needs a starting value:
+// every call writes each region before reading it.
+constexpr int64_t kScratchMaxTokens = 128;
+constexpr int64_t kScratchBytes = layout(kScratchMaxTokens).total;  // about 6.6 MB
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+int device_scratch(void **ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(LM_ELAUNCH, std::string("hipGetDevice failed: ") + hipGetErrorString(e));
+  LM_REQUIRE(dev >= 0 && dev < kMaxDevices, LM_EINVAL, "device index beyond 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(LM_ELAUNCH, std::string("hipGetSymbolAddress(scratch) failed: ") +
+                                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return LM_OK;
+}
+}  // namespace
+
 extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t tokens,
                                     int64_t hidden, int64_t inter, int64_t experts, int64_t top_k,
                                     float eps, void *workspace, int64_t workspace_bytes,
@@ -1115,4 +1154,21 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
     return check_launch("export_routing_kernel");
   }
   return LM_OK;
+}
+
+extern "C" int64_t lm_moe_static_max_tokens(void) { return kScratchMaxTokens; }
+
+extern "C" int lm_moe_layer_forward_static(const lm_moe_layer *layer, void *h, int64_t tokens,
+                                           int64_t hidden, int64_t inter, int64_t experts,
+                                           int64_t top_k, float eps, int32_t *ids_out,
+                                           void *weights_out, void *const *phase_events,
+                                           void *stream) {
+  LM_REQUIRE(tokens >= 1, LM_EINVAL, "invalid token count");
+  LM_REQUIRE(tokens <= kScratchMaxTokens, LM_ENOMEM,
+             "token count exceeds the static scratch (128 tokens); use lm_moe_layer_forward "
+             "with a caller workspace");
+  void *ws = nullptr;
+  if (int rc = device_scratch(&ws)) return rc;
+  return lm_moe_layer_forward(layer, h, tokens, hidden, inter, experts, top_k, eps, ws,
+                              kScratchBytes, ids_out, weights_out, phase_events, stream);
 }

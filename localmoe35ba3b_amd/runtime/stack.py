@@ -161,6 +161,18 @@ class MoEStack:
             return raw
         return raw.view(-1, {'H': self.H, 'I': self.I, 'K': self.K}[inner])
 
+    def layer_forward_static(self, h, l, ids_out=None, weights_out=None):
+        """layer_forward through lm_moe_layer_forward_static: the workspace is
+        the library's own device array, so the call allocates nothing (at most
+        lm_moe_static_max_tokens() tokens; calls on one device must not
+        overlap)."""
+        if h.dtype != torch.bfloat16 or not h.is_contiguous() or h.shape[-1] != self.H:
+            raise ValueError('expected contiguous bf16 [tokens, 2048] hidden states')
+        _lib.call('lm_moe_layer_forward_static', ctypes.byref(self._structs[l]), h.data_ptr(),
+                  h.shape[0], self.H, self.I, self.E, self.K, EPS, _lib.ptr(ids_out),
+                  _lib.ptr(weights_out), None, _lib.stream(h.device))
+        return h
+
     def forward(self, h, layers=None):
         for l in range(self.L if layers is None else layers):
             self.layer_forward(h, l)
