@@ -268,6 +268,99 @@ __device__ __forceinline__ float row_sum_f32(float v) {
   return v;
 }
 
+// ------------------------------------------------------------ wave selection
+// Lane l's copy of lane l ^ D's value (D = 1, 2, 4, 8, 16, 32): quad
+// permutations for 1 and 2, the two row shifts by 4 written into alternate
+// 4-lane banks for 4, the row rotation by 8, a swizzle within 32 lanes for 16
+// and a permute across the wave for 32.
+template <int D>
+__device__ __forceinline__ uint32_t lane_xor_u32(uint32_t v) {
+  if constexpr (D == 1) {
+    return dpp_u32<0xB1>(v);
+  } else if constexpr (D == 2) {
+    return dpp_u32<0x4E>(v);
+  } else if constexpr (D == 4) {
+    int t = __builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xF, 0x5, false);  // row_shl:4
+    t = __builtin_amdgcn_update_dpp(t, (int)v, 0x114, 0xF, 0xA, false);      // row_shr:4
+    return (uint32_t)t;
+  } else if constexpr (D == 8) {
+    return dpp_u32<0x128>(v);  // row_ror:8
+  } else if constexpr (D == 16) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (16 << 10) | 0x1F);
+  } else {
+    static_assert(D == 32, "lane_xor_u32: D in {1, 2, 4, 8, 16, 32}");
+    return (uint32_t)__shfl_xor((int)v, 32, 64);
+  }
+}
+// Lane l's copy of lane l ^ M for the mirror partners of the top-8 merges:
+// 15 (row mirror), 23 (swizzle within 32 lanes), 39 (permute across the wave).
+template <int M>
+__device__ __forceinline__ uint32_t lane_mirror_u32(uint32_t v) {
+  if constexpr (M == 15) {
+    return dpp_u32<0x140>(v);
+  } else if constexpr (M == 23) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (23 << 10) | 0x1F);
+  } else {
+    static_assert(M == 39, "lane_mirror_u32: M in {15, 23, 39}");
+    return (uint32_t)__shfl_xor((int)v, 39, 64);
+  }
+}
+template <int D>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) { return lane_xor_u32<D>(v); }
+template <int D>
+__device__ __forceinline__ unsigned long long lane_xor(unsigned long long v) {
+  return ((unsigned long long)lane_xor_u32<D>((uint32_t)(v >> 32)) << 32) |
+         lane_xor_u32<D>((uint32_t)v);
+}
+template <int M>
+__device__ __forceinline__ uint32_t lane_mirror(uint32_t v) { return lane_mirror_u32<M>(v); }
+template <int M>
+__device__ __forceinline__ unsigned long long lane_mirror(unsigned long long v) {
+  return ((unsigned long long)lane_mirror_u32<M>((uint32_t)(v >> 32)) << 32) |
+         lane_mirror_u32<M>((uint32_t)v);
+}
+
+// Compare-exchange with lane l ^ J: the lower lane of the pair keeps the
+// larger key when `desc`, the smaller otherwise.
+template <int J, typename T>
+__device__ __forceinline__ T lane_cx(T k, int lane, bool desc) {
+  const T p = lane_xor<J>(k);
+  const T hi = k > p ? k : p, lo = k > p ? p : k;
+  return (((lane & J) == 0) == desc) ? hi : lo;
+}
+// Bitonic sort of every 8-lane block, descending.
+template <typename T>
+__device__ __forceinline__ T sort8_desc(T k, int lane) {
+  k = lane_cx<1>(k, lane, (lane & 2) == 0);
+  k = lane_cx<2>(k, lane, (lane & 4) == 0);
+  k = lane_cx<1>(k, lane, (lane & 4) == 0);
+  k = lane_cx<4>(k, lane, true);
+  k = lane_cx<2>(k, lane, true);
+  return lane_cx<1>(k, lane, true);
+}
+// Every 8-lane block of a group holds the same list sorted descending; the
+// partner group's list is read mirrored (lane ^ M, M = group size * 2 - 1
+// folded into the block), so position i meets partner position 7 - i.  The
+// larger of each pair are the 8 largest of both lists in bitonic order; a
+// half-cleaner sorts them descending in every block of the merged group.
+template <int M, typename T>
+__device__ __forceinline__ T merge_top8(T k, int lane) {
+  const T p = lane_mirror<M>(k);
+  k = k > p ? k : p;
+  k = lane_cx<4>(k, lane, true);
+  k = lane_cx<2>(k, lane, true);
+  return lane_cx<1>(k, lane, true);
+}
+// The 8 largest of the wave's 64 keys (one per lane, distinct), sorted
+// descending in every 8-lane block: lane l holds the one of rank l & 7.
+template <typename T>
+__device__ __forceinline__ T wave_top8(T k, int lane) {
+  k = sort8_desc(k, lane);
+  k = merge_top8<15>(k, lane);
+  k = merge_top8<23>(k, lane);
+  return merge_top8<39>(k, lane);
+}
+
 // LDS scratch of one top-k wave, in 64-bit words: 4 rows x 16 candidates
 // plus 16 selected probabilities.
 constexpr int kTopkScratch = 80;

@@ -123,7 +123,7 @@ __global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
     const float xsv = (!QUANT && a.xs) ? a.xs[(int64_t)(rv.xrow + ti / G) * G + ti % G] : 0.0f;
     const int tw = min(th, rv.rvalid * G - 1);
     const float wsv = PARTIALS ? 0.0f : rv.s[(int64_t)rv.map(tw / G) * G + tw % G];
-    RowLoads<kGemvLoads> L;
+    RowLoads<kGemvLoads, kGemvThreads> L;
     L.issue(rv.rvalid, G, row_ptr);
     if constexpr (QUANT)
       qst.store(K, xq, xs);
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_kernel(GemvArgs a) {
     cst.load(xsrc, a.ldx * 2, M, K * 2);
     const int tw = min((int)threadIdx.x, rv.rvalid * G - 1);
     const float wsv = rv.s[(int64_t)rv.map(tw / G) * G + tw % G];
-    RowLoads<kGemvLoads> L;
+    RowLoads<kGemvLoads, kGemvThreads> L;
     L.issue(rv.rvalid, G, row_ptr);
     cst.store(reinterpret_cast<unsigned char *>(xl));
     if ((int)threadIdx.x < rv.rvalid * G) ws[threadIdx.x] = wsv;

@@ -79,8 +79,10 @@ __device__ __forceinline__ void stream_rows(int R, int G, RowPtr row_ptr, Body b
 // past the end read pair 0 again (a valid address) and are flagged !ok.
 // All lanes of an octet share one (row, group) pair and hence one ok flag.
 // Branch-free issue keeps the compiler's wait counts exact, so code that
-// needs only older loads does not wait for these.
-template <int LOADS>
+// needs only older loads does not wait for these.  THREADS is the
+// workgroup size the kernel is launched with (a constant, so the issue does
+// not wait for the block-size kernel argument).
+template <int LOADS, int THREADS = 256>
 struct RowLoads {
   u32x4 w[LOADS];
   int r[LOADS], g[LOADS], f[LOADS];
@@ -88,9 +90,10 @@ struct RowLoads {
 
   template <typename RowPtr>
   __device__ __forceinline__ void issue(int R, int G, RowPtr row_ptr) {
+    static_assert(THREADS % 64 == 0, "whole waves");
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int nwaves = blockDim.x >> 6;
+    constexpr int nwaves = THREADS >> 6;
     const int sub = lane & 7;
     const int total = R * G;
     const int ninstr = (total + 7) >> 3;

@@ -105,13 +105,16 @@ struct LayerArgs {
 };
 
 // ------------------------------------------------------------------ decode
-// RMSNorm of one row of kH bf16 values into LDS floats (bf16-rounded values).
-__device__ __forceinline__ void norm_row_to_lds(const uint16_t *h, const float *nw, float eps,
-                                                float *xf, float *red) {
+// RMSNorm of one row of kH bf16 values (HF:807-815).  Thread t passes in
+// its chunk, values 8 t .. 8 t + 7, and receives them normalized and rounded
+// to bf16.  Fixed
+// reduction order (per-thread sum, 64-lane xor butterfly, the 4 wave sums
+// left to right, IEEE 1/sqrtf), which the oracle restates.
+__device__ __forceinline__ void norm_row(u32x4 raw, const float *nw, float eps, float *red,
+                                         float y[kH / 256]) {
   constexpr int PER = kH / 256;
   const int t = threadIdx.x;
   float v[PER];
-  const u32x4 raw = ldg16(h + t * PER);
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -127,32 +130,51 @@ __device__ __forceinline__ void norm_row_to_lds(const uint16_t *h, const float *
   const float r = 1.0f / sqrtf(tot / (float)kH + eps);
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    float y = v[j] * r;
-    if (nw) y = y * (1.0f + nw[t * PER + j]);
-    xf[t * PER + j] = round_bf16(y);
+    float yy = v[j] * r;
+    if (nw) yy = yy * (1.0f + nw[t * PER + j]);
+    y[j] = round_bf16(yy);
   }
+}
+
+// The normalized row as LDS floats (bf16-rounded values); `raw` is thread
+// t's chunk of the row (values 8 t .. 8 t + 7).
+__device__ __forceinline__ void norm_row_to_lds(u32x4 raw, const float *nw, float eps, float *xf,
+                                                float *red) {
+  constexpr int PER = kH / 256;
+  float y[PER];
+  norm_row(raw, nw, eps, red, y);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) xf[threadIdx.x * PER + j] = y[j];
   __syncthreads();
 }
 
-// Router logits of the decode token: blocks 0..E/4-1 take one expert per
-// wave (the router row is loaded before the RMSNorm so its HBM latency
-// overlaps the norm); block E/4 computes the shared-expert gate logit.
-// Every block normalizes the row itself, so blocks 0..H/128-1 also write one
-// 128-wide group of the normalized row and its W8A8 quantization (no block
-// carries a serial tail).  No inter-block sync.
+constexpr int kGuPairs = 8;  // routed SwiGLU columns per gate_up workgroup
+constexpr int kRouterBlocks = kE / 4;  // one router expert per wave, + 1 workgroup for the gate logit
+
+// Decode layer, first kernel: router logits of the token (workgroups
+// 0 .. E/4 - 1, one expert per wave) and the shared-expert gate logit
+// (workgroup E/4).  The hidden row is requested first and the router rows
+// right after it, so the RMSNorm waits for the row alone and the router
+// rows' HBM latency overlaps it.  Every workgroup normalizes the row itself,
+// so workgroups 0 .. H/128 - 1 also write one 128-wide group of the
+// normalized row and its W8A8 quantization.  No inter-workgroup sync.
 __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
   __shared__ float xf[kH];
   __shared__ float red[4];
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  const bool routed = blockIdx.x < kE / 4;
-  const int e = blockIdx.x * 4 + wave;
+  const bool routed = blockIdx.x < kRouterBlocks;
+  // Workgroup b runs on XCD b % 8.  Expert groups are dealt out so that the
+  // 8 workgroups writing one 128-byte line of logits share an XCD.
+  const int b = blockIdx.x;
+  const int e = ((b & 7) * (kRouterBlocks / 8) + (b >> 3)) * 4 + wave;
   const uint16_t *wrow = routed ? a.router_w + (int64_t)e * kH : a.gate_w;
+  const u32x4 hrow = ldg16(a.h + t * (kH / 256));
   u32x4 wv[kH / 512];
 #pragma unroll
   for (int j = 0; j < kH / 512; ++j) wv[j] = ldg16(wrow + lane * 8 + j * 512);
-  norm_row_to_lds(a.h, a.norm_w, a.eps, xf, red);
+  norm_row_to_lds(hrow, a.norm_w, a.eps, xf, red);
 
   if (blockIdx.x < kH / 128) {
     const int g = blockIdx.x;
@@ -203,31 +225,73 @@ __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
   }
 }
 
-// Top-8 of the decode token from the router logits (one wave), ascending
-// expert order for the combine.  Every decode gate_up workgroup runs it on
-// the same inputs, so all of them agree bit for bit; workgroup (0, 0)
-// publishes the result for the down kernel and the caller.
-__device__ __forceinline__ void decode_topk(const LayerArgs &a, int *sel, float *selw) {
-  __shared__ int64_t sid[kTopK];
-  __shared__ uint16_t swt[kTopK];
-  __shared__ unsigned long long scratch[kTopkScratch];
-  const int t = threadIdx.x;
-  if (t < 64) {
-    topk_wave(a.logits, kE, kTopK, t, scratch, sid, swt);
-    wave_lds_sync();
-    if (t < kTopK) {  // route t: its rank in ascending id order is its combine slot
-      const int64_t id = clamp_index(sid[t], kE);
-      const uint16_t wb = swt[t];
-      const int rank = combine_slot(sid, kTopK, t);
+// Top-8 of the decode token over the 256 router logits (HF:770-774), with
+// all four waves of the workgroup: thread t holds expert t's logit v, and
+// every wave selects the 8 largest keys (logit desc, id asc) of its 64
+// experts; wave 0 then merges the four lists while wave 1 forms the softmax
+// denominator from v4, lane l's logits of experts 4 l .. 4 l + 3.  The
+// arithmetic (denominator order, fp32 softmax, renormalisation in rank
+// order, bf16 weights) is topk_wave's, so ids and weights equal the
+// single-wave selection bit for bit.  Fills sel/selw in combine order
+// (ascending expert id); workgroup (0, 0) publishes the routing for the down
+// kernel and the caller.  Every gate_up workgroup runs it on the same
+// inputs, so all of them agree.
+template <class KT>
+__device__ __forceinline__ void decode_select(const LayerArgs &a, float v, const float v4[4],
+                                              int *sel, float *selw) {
+  using T = typename KT::T;
+  __shared__ T lists[4 * kTopK];
+  __shared__ float denom_s;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  T k = wave_top8(KT::make(v, t), lane);
+  if (lane < kTopK) lists[wave * kTopK + lane] = k;
+  __syncthreads();
+  if (wave == 0) {
+    k = lists[lane & 31];
+    k = merge_top8<15>(k, lane);
+    k = merge_top8<23>(k, lane);
+  } else if (wave == 1) {
+    T top = lists[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const T o = lists[w * kTopK];
+      top = o > top ? o : top;
+    }
+    const float mx = KT::value(top);
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part += expf(v4[j] - mx);
+    part = row_sum_f32(part);
+    const float d = (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 0)) +
+                     __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16))) +
+                    (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 32)) +
+                     __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 48)));
+    if (lane == 0) denom_s = d;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const float mx = KT::value(KT::readlane(k, 0));
+    const float pe = expf(KT::value(k) - mx) / denom_s;
+    float psum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), 0));
+#pragma unroll
+    for (int i = 1; i < kTopK; ++i)
+      psum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), i));
+    const uint16_t wb = f32_to_bf16_bits(pe / psum);
+    const int id = clamp_index32(KT::index(k), kE);
+    int rank = 0;  // combine slot: rank of the id in ascending order (the ids are distinct)
+#pragma unroll
+    for (int i = 0; i < kTopK; ++i)
+      rank += clamp_index32(KT::index(KT::readlane(k, i)), kE) < id ? 1 : 0;
+    if (lane < kTopK) {
       const float w = bf16_bits_to_f32(wb);
-      sel[rank] = (int)id;
+      sel[rank] = id;
       selw[rank] = w;
-      if (blockIdx.x == 0 && blockIdx.y == 0) {
-        a.ids[t] = id;
-        a.wts[t] = wb;
-        if (a.ids_out) a.ids_out[t] = (int)id;
-        if (a.wts_out) a.wts_out[t] = wb;
-        a.sel[rank] = (int)id;
+      if (blockIdx.x == 0) {
+        a.ids[lane] = id;
+        a.wts[lane] = wb;
+        if (a.ids_out) a.ids_out[lane] = id;
+        if (a.wts_out) a.wts_out[lane] = wb;
+        a.sel[rank] = id;
         a.selw[rank] = w;
       }
     }
@@ -235,80 +299,104 @@ __device__ __forceinline__ void decode_topk(const LayerArgs &a, int *sel, float 
   __syncthreads();
 }
 
-// gate_up of slot blockIdx.y (0..7 routed W8A8, 8 = shared W8A16), 8 output
-// columns per block: rows n0..n0+7 (gate) and kI+n0.. (up), K = kH.  The W8A8
-// per-group terms (f32(p) * xs_g) * ws_g are formed by the lane that owns the
-// partial and summed in ascending group order by the epilogue (w8a8.py:40).
-constexpr int kGuPairs = 8;
+// Decode layer, second kernel: gate_up of one routed slot (W8A8),
+// 8 output columns per workgroup: rows n0..n0+7 (gate) and kI+n0.. (up),
+// K = kH, after the top-8.  The W8A8 per-group terms (f32(p) * xs_g) * ws_g
+// are formed by the lane that owns the partial and summed in ascending group
+// order by the epilogue (w8a8.py:40).  The grid is 512 workgroups, two per
+// CU; each also computes one column of the shared expert's gate_up + SwiGLU (W8A16 on the normalized row), whose inputs do
+// not depend on the routing: they are requested behind the logits and
+// consumed while the routed weights are in flight.
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
   constexpr int G = kH / 128;
   constexpr int R = 2 * kGuPairs;
   static_assert(R * G == 256, "one group scale per thread");
-  __shared__ __align__(16) unsigned char xbuf[kH * 2];
+  static_assert(kI / kGuPairs * kTopK == kI, "one shared column per workgroup");
+  static_assert(kI / kGuPairs == 64 && kTopK == 8, "the XCD deal below");
+  __shared__ __align__(16) int8_t xbuf[kH];
+  __shared__ __align__(16) uint16_t xb[kH];
   __shared__ float xs[G];
   __shared__ float wsc[R * G];
   __shared__ float term[R * G];
+  __shared__ float wsh[2 * G];
+  __shared__ float tsh[2 * G];
   __shared__ int sel[kTopK];
   __shared__ float selw[kTopK];
   const int t = threadIdx.x;
-  const int slot = blockIdx.y;
-  const bool shared = slot == kTopK;
-  const int n0 = blockIdx.x * kGuPairs;
+  // Workgroup b runs on XCD x = b % 8.  (slot, column) tiles are dealt out
+  // so that the 8 workgroups writing one 128-byte line of a SwiGLU row (64
+  // columns), and the 64 writing one line of the shared row, share an XCD.
+  const int b = blockIdx.x, x = b & 7, k = b >> 3;
+  const int pair = x + 8 * (k >> 3);  // (slot, line) pair: 8 slots x 8 lines
+  const int slot = pair >> 3;
+  const int n0 = ((pair & 7) * 8 + (k & 7)) * kGuPairs;
+  const int nsh = x * 64 + k;  // shared column of this workgroup
   const RowMap map{n0, kI + n0, kGuPairs};
-  // Weights stream straight into registers; the block's 256 group scales
-  // come in as one dword per thread, so every in-flight load slot of a lane
-  // but one carries 16 weight bytes.
+  const RowMap map_sh{nsh, kI + nsh, 1};
+  // The logits first, then the quantized activation row, then the shared
+  // column's inputs; the routed weights follow as soon as the selection is
+  // known.  (Loads complete in issue order, so the selection waits for the
+  // logits and the activation row alone.)
+  // Every load is issued by every thread from a valid address (only the
+  // stores are guarded): a load inside a branch makes the compiler wait for
+  // all loads in flight where the branch joins.
+  const float v = a.logits[t];
+  const float4 f4 = *reinterpret_cast<const float4 *>(a.logits + (t & 63) * 4);
+  const float v4[4] = {f4.x, f4.y, f4.z, f4.w};  // used by wave 1
+  const u32x4 xv = ldg16(a.xq + (t & (kH / 16 - 1)) * 16);
+  const float xsv = a.xs[t & (G - 1)];
+  const u32x4 xnv = ldg16(a.xn + t * (kH / 256));
+  const int8_t *wq_sh = a.gu_q + (int64_t)kE * a.gu_qes;
+  RowLoads<1> Ls;
+  Ls.issue(2, G, [&](int r) { return wq_sh + (int64_t)map_sh(r) * kH; });
+  const int fs = t & (2 * G - 1);
+  const float ssv = a.gu_s[(int64_t)kE * a.gu_ses + (int64_t)map_sh(fs / G) * G + fs % G];
+  if (a.router_bias)  // biased logits are fp32 values: 64-bit keys
+    decode_select<Key64>(a, v, v4, sel, selw);
+  else  // bf16 logits: 32-bit keys order them identically
+    decode_select<Key32>(a, v, v4, sel, selw);
+  const int e = clamp_index32(sel[slot], kE);
+  const int8_t *wq = a.gu_q + (int64_t)e * a.gu_qes;
+  const float my_scale = a.gu_s[(int64_t)e * a.gu_ses + (int64_t)map(t / G) * G + t % G];
   RowLoads<8> L;
-  float my_scale = 0.0f;
-  auto issue = [&](int e) {
-    const int8_t *wq = a.gu_q + (int64_t)e * a.gu_qes;
-    my_scale = a.gu_s[(int64_t)e * a.gu_ses + (int64_t)map(t / G) * G + t % G];
-    L.issue(R, G, [&](int r) { return wq + (int64_t)map(r) * kH; });
-  };
-  // Everything that does not depend on the routing is requested before the
-  // top-k: the shared slot's weights and every slot's activation row (kept
-  // in registers until the top-k is done).
-  u32x4 xv = u32x4{0u, 0u, 0u, 0u};
-  float xsv = 0.0f;
-  if (shared) {
-    xv = ldg16(a.xn + t * 8);
-    issue(kE);
-  } else {
-    if (t < kH / 16) xv = ldg16(a.xq + t * 16);
-    if (t < G) xsv = a.xs[t];
-  }
-  if (!shared) {
-    decode_topk(a, sel, selw);
-    issue(clamp_index32(sel[slot], kE));
-  }
-  if (shared) {
-    reinterpret_cast<u32x4 *>(xbuf)[t] = xv;
-  } else {
-    if (t < kH / 16) reinterpret_cast<u32x4 *>(xbuf)[t] = xv;
-    if (t < G) xs[t] = xsv;
-  }
-  wsc[t] = my_scale;
-  __syncthreads();
+  L.issue(R, G, [&](int r) { return wq + (int64_t)map(r) * kH; });
 
+  // shared column (its inputs arrived during the selection)
+  reinterpret_cast<u32x4 *>(xb)[t] = xnv;
+  if (t < 2 * G) wsh[t] = ssv;
+  if (t < kH / 16) reinterpret_cast<u32x4 *>(xbuf)[t] = xv;
+  if (t < G) xs[t] = xsv;
+  __syncthreads();
   const int sub = t & 7;
-  if (shared) {
-    const uint16_t *x16 = reinterpret_cast<const uint16_t *>(xbuf);
-    L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
-      uint32_t wd[8];
-      dequant16<BF16>(w, wsc[f], wd);
-      const uint16_t *xp = x16 + g * 128 + sub * 16;
-      const float p = octet_sum_f32(dot16_w16<BF16>(wd, *reinterpret_cast<const u32x4 *>(xp),
-                                                    *reinterpret_cast<const u32x4 *>(xp + 8)));
-      if (ok && sub == 0) term[f] = p;
-    });
-  } else {
-    const int8_t *x8 = reinterpret_cast<const int8_t *>(xbuf);
-    L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
-      const int p = octet_sum_i32(
-          dot16_i8(w, *reinterpret_cast<const u32x4 *>(x8 + g * 128 + sub * 16)));
-      if (ok && sub == 0) term[f] = mul_rn(mul_rn((float)p, xs[g]), wsc[f]);
-    });
+  Ls.consume([&](u32x4 w, int r, int g, int f, bool ok) {
+    uint32_t wd[8];
+    dequant16<BF16>(w, wsh[f], wd);
+    const uint16_t *xp = xb + g * 128 + sub * 16;
+    const float p = octet_sum_f32(dot16_w16<BF16>(wd, *reinterpret_cast<const u32x4 *>(xp),
+                                                  *reinterpret_cast<const u32x4 *>(xp + 8)));
+    if (ok && sub == 0) tsh[f] = p;
+  });
+  __syncthreads();
+  if (t == 64) {
+    float sg = 0.0f, su = 0.0f;
+    for (int g = 0; g < G; ++g) {
+      sg = add_rn(sg, tsh[g]);
+      su = add_rn(su, tsh[G + g]);
+    }
+    const float gate = round_bf16(sg), up = round_bf16(su);
+    a.hbuf[kTopK * kI + nsh] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
   }
+  // The scales of the pairs a wave consumes are the ones its own threads
+  // loaded (pair f = thread f), so they are handed over within the wave and
+  // no workgroup barrier waits for them.
+  wsc[t] = my_scale;
+  wave_lds_sync();
+
+  L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
+    const int p =
+        octet_sum_i32(dot16_i8(w, *reinterpret_cast<const u32x4 *>(xbuf + g * 128 + sub * 16)));
+    if (ok && sub == 0) term[f] = mul_rn(mul_rn((float)p, xs[g]), wsc[f]);
+  });
   __syncthreads();
   if (t < kGuPairs) {
     float sg = 0.0f, su = 0.0f;
@@ -321,13 +409,22 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
   }
 }
 
-// down rows of all 9 slots for 8 output columns, combine, gated shared add,
-// residual add.  The 8 routed SwiGLU rows are quantized per row (w8a8.quantize
-// on [8, kI]) in one parallel pass: thread t owns 16 values of row t / 32.
+// Decode layer, third kernel: down rows of the 8 routed experts and of the
+// shared expert for 8 output columns c0 .. c0 + 7 (W8A8 on the row-quantized
+// SwiGLU rows / W8A16), then the ascending-expert bf16 combine
+// (int8.py:240-250), the gated shared add and the residual add, in place.
+// The expert ids are requested first (scalar loads); everything that does
+// not depend on them - the shared expert's rows and scales, its SwiGLU row,
+// the residual columns, the gate logit - follows at once, and the routed
+// weights as soon as the ids land.  The 8 routed SwiGLU rows are quantized
+// per row (w8a8.quantize on [8, kI]) in one parallel pass: thread t owns
+// 16 values of row t / 32.
 constexpr int kDnCols = 8;
 __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   constexpr int G = kI / 128;
-  constexpr int R = (kTopK + 1) * kDnCols;
+  constexpr int RR = kTopK * kDnCols;  // routed rows
+  constexpr int R = RR + kDnCols;      // + the shared expert's
+  static_assert(RR * G == 256, "one routed group scale per thread");
   __shared__ __align__(16) int8_t xq[kTopK * kI];
   __shared__ float xs[kTopK * G];
   __shared__ __align__(16) uint16_t xsh[kI];
@@ -335,33 +432,47 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   __shared__ float wsc[R * G];
   __shared__ float selw[kTopK];
   const int t = threadIdx.x;
-  const int c0 = blockIdx.x * kDnCols;
+  // Workgroup b runs on XCD b % 8; column tiles are dealt out so that the 8
+  // workgroups writing one 128-byte line of h (64 columns) share an XCD.
+  const int b = blockIdx.x;
+  const int c0 = (((b & 7) * 4 + ((b >> 3) >> 3)) * 8 + ((b >> 3) & 7)) * kDnCols;
   int ex[kTopK];
 #pragma unroll
   for (int s = 0; s < kTopK; ++s) ex[s] = a.sel[s];
-  auto expert_of = [&](int r) { return decode_row_expert(ex, kTopK, kDnCols, kE, r); };
-  // The SwiGLU rows are requested together with the expert ids; the weight
-  // loads follow as soon as the ids arrive.
+  __builtin_amdgcn_sched_barrier(0);  // the ids are requested before anything else
+  // Every load is issued by every thread from a valid address (only the
+  // stores are guarded): a load inside a branch makes the compiler wait for
+  // all loads in flight where the branch joins.  Loads complete in issue
+  // order, so the routed SwiGLU rows (quantized while the weights stream)
+  // come first, then the routed scales and weights, and last the shared
+  // expert's inputs, which are used after the routed rows.
   const int row = t >> 5, col = (t & 31) * 16;
   const u32x4 h0 = ldg16(a.hbuf + row * kI + col);
   const u32x4 h1 = ldg16(a.hbuf + row * kI + col + 8);
-  const u32x4 hsh = t < kI / 8 ? ldg16(a.hbuf + kTopK * kI + t * 8) : u32x4{0u, 0u, 0u, 0u};
-  const float wsel = t < kTopK ? a.selw[t] : 0.0f;
-  // the block's R * G group scales (one or two dwords per thread), then the
-  // weights, so the scales are not queued behind them
-  float sv0 = 0.0f, sv1 = 0.0f;
-  {
-    const int f0 = t, f1 = t + 256;
-    sv0 = a.dn_s[(int64_t)expert_of(f0 / G) * a.dn_ses + (int64_t)(c0 + (f0 / G) % kDnCols) * G +
-                 f0 % G];
-    if (f1 < R * G)
-      sv1 = a.dn_s[(int64_t)expert_of(f1 / G) * a.dn_ses +
-                   (int64_t)(c0 + (f1 / G) % kDnCols) * G + f1 % G];
-  }
-  RowLoads<12> L;
-  L.issue(R, G, [&](int r) {
-    return a.dn_q + (int64_t)expert_of(r) * a.dn_qes + (int64_t)(c0 + r % kDnCols) * kI;
+  const float wsel = a.selw[t & (kTopK - 1)];
+  // Routed pairs f = row * G + group: wave w owns pairs 64 w .. 64 w + 63,
+  // i.e. the rows of slots 2 w and 2 w + 1, and thread f loads the scale of
+  // pair f.
+  const int w2 = 2 * __builtin_amdgcn_readfirstlane(t >> 6);
+  const int8_t *q_lo = a.dn_q + (int64_t)clamp_index32(ex[w2], kE) * a.dn_qes + (int64_t)c0 * kI;
+  const int8_t *q_hi =
+      a.dn_q + (int64_t)clamp_index32(ex[w2 + 1], kE) * a.dn_qes + (int64_t)c0 * kI;
+  const float *s_own = a.dn_s + (int64_t)clamp_index32(ex[t >> 5], kE) * a.dn_ses +
+                       (int64_t)c0 * G;
+  const float sv = s_own[t & (kDnCols * G - 1)];
+  RowLoads<8> L;
+  L.issue(RR, G, [&](int r) {
+    return ((r / kDnCols) & 1 ? q_hi : q_lo) + (int64_t)(r % kDnCols) * kI;
   });
+  RowLoads<1> Ls;  // the shared expert's 8 rows
+  Ls.issue(kDnCols, G, [&](int r) {
+    return a.dn_q + (int64_t)kE * a.dn_qes + (int64_t)(c0 + r) * kI;
+  });
+  const int fs = t & (kDnCols * G - 1);
+  const float ssv = a.dn_s[(int64_t)kE * a.dn_ses + (int64_t)(c0 + fs / G) * G + fs % G];
+  const u32x4 hsh = ldg16(a.hbuf + kTopK * kI + (t & (kI / 8 - 1)) * 8);
+  const uint16_t hres = a.h[c0 + (t & (kDnCols - 1))];
+  const float glv = a.gl[0];
   __builtin_amdgcn_sched_barrier(0);  // keep the quantization below the weight loads
 
   // Row quantization of hbuf[0..7]: 16 values per thread, a 128-group is
@@ -392,28 +503,31 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   }
   *reinterpret_cast<u32x4 *>(xq + row * kI + col) = packed;
   if ((t & 7) == 0) xs[row * G + col / 128] = sc;
-  wsc[t] = sv0;
-  if (t + 256 < R * G) wsc[t + 256] = sv1;
-  if (t < kI / 8) reinterpret_cast<u32x4 *>(xsh)[t] = hsh;
   if (t < kTopK) selw[t] = wsel;
   __syncthreads();
 
+  // The routed scales of the pairs a wave consumes are the ones its own
+  // threads loaded (pair f = thread f): a wave-local hand-off, so the
+  // workgroup barrier above did not wait for them.
+  wsc[t] = sv;
+  wave_lds_sync();
   const int sub = t & 7;
   L.consume([&](u32x4 w, int r, int g, int f, bool ok) {
-    const float scl = wsc[f];
     const int s = r / kDnCols;  // uniform across the wave instruction
-    if (s < kTopK) {
-      const int p = octet_sum_i32(
-          dot16_i8(w, *reinterpret_cast<const u32x4 *>(xq + s * kI + g * 128 + sub * 16)));
-      if (ok && sub == 0) term[f] = mul_rn(mul_rn((float)p, xs[s * G + g]), scl);
-    } else {
-      uint32_t wd[8];
-      dequant16<BF16>(w, scl, wd);
-      const uint16_t *xp = xsh + g * 128 + sub * 16;
-      const float p = octet_sum_f32(dot16_w16<BF16>(wd, *reinterpret_cast<const u32x4 *>(xp),
-                                                    *reinterpret_cast<const u32x4 *>(xp + 8)));
-      if (ok && sub == 0) term[f] = p;
-    }
+    const int p = octet_sum_i32(
+        dot16_i8(w, *reinterpret_cast<const u32x4 *>(xq + s * kI + g * 128 + sub * 16)));
+    if (ok && sub == 0) term[f] = mul_rn(mul_rn((float)p, xs[s * G + g]), wsc[f]);
+  });
+  if (t < kDnCols * G) wsc[RR * G + t] = ssv;
+  if (t < kI / 8) reinterpret_cast<u32x4 *>(xsh)[t] = hsh;
+  __syncthreads();
+  Ls.consume([&](u32x4 w, int r, int g, int f, bool ok) {
+    uint32_t wd[8];
+    dequant16<BF16>(w, wsc[RR * G + f], wd);
+    const uint16_t *xp = xsh + g * 128 + sub * 16;
+    const float p = octet_sum_f32(dot16_w16<BF16>(wd, *reinterpret_cast<const u32x4 *>(xp),
+                                                  *reinterpret_cast<const u32x4 *>(xp + 8)));
+    if (ok && sub == 0) term[RR * G + f] = p;
   });
   __syncthreads();
   if (t < kDnCols) {
@@ -425,12 +539,11 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
       acc = round_bf16(acc + round_bf16(round_bf16(v8) * selw[s]));
     }
     float vs = 0.0f;
-    for (int g = 0; g < G; ++g) vs += term[(kTopK * kDnCols + t) * G + g];
+    for (int g = 0; g < G; ++g) vs += term[(RR + t) * G + g];
     const float vsh = round_bf16(vs);
-    const float sig = round_bf16(sigmoid_f32(a.gl[0]));
+    const float sig = round_bf16(sigmoid_f32(glv));
     const float out = round_bf16(acc + round_bf16(sig * vsh));
-    const int n = c0 + t;
-    a.h[n] = f32_to_bf16_bits(bf16_bits_to_f32(a.h[n]) + out);
+    a.h[c0 + t] = f32_to_bf16_bits(bf16_bits_to_f32(hres) + out);
   }
 }
 
@@ -469,7 +582,7 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a, int
     if (tok < kE) router_row_norm();
     return;
   }
-  norm_row_to_lds(a.h + (int64_t)tok * kH, a.norm_w, a.eps, xf, red);
+  norm_row_to_lds(ldg16(a.h + (int64_t)tok * kH + t * PER), a.norm_w, a.eps, xf, red);
   {
     float ss = 0.0f;
 #pragma unroll
@@ -1103,12 +1216,13 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
 
   if (tokens == 1) {
     if (int rc = mark(0)) return rc;
-    decode_router_kernel<<<kE / 4 + 1, 256, 0, st>>>(a);
+    decode_router_kernel<<<kRouterBlocks + 1, 256, 0, st>>>(a);
     if (int rc = check_launch("decode_router_kernel")) return rc;
     if (int rc = mark(1)) return rc;
-    decode_gate_up_kernel<<<dim3(kI / kGuPairs, kTopK + 1), 256, 0, st>>>(a);
+    decode_gate_up_kernel<<<kI / kGuPairs * kTopK, 256, 0, st>>>(a);
     if (int rc = check_launch("decode_gate_up_kernel")) return rc;
     if (int rc = mark(2)) return rc;
+    static_assert(kH / kDnCols == 256, "the XCD deal of decode_down_kernel");
     decode_down_kernel<<<kH / kDnCols, 256, 0, st>>>(a);
     if (int rc = check_launch("decode_down_kernel")) return rc;
     return mark(3);
