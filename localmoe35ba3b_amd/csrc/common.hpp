@@ -179,8 +179,20 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // ------------------------------------------------------------ loads
-__device__ __forceinline__ u32x4 ldg16(const void *p) {
-  return *reinterpret_cast<const u32x4 *>(p);
+// Loads from global memory through global address-space pointers, so that
+// they compile to global (not flat) loads even where the pointer itself was
+// loaded from memory (descriptor tables): a flat load counts on the LDS
+// counter as well, and every later LDS or scalar wait would wait for it.
+template <typename V>
+__device__ __forceinline__ V ldg(const void *p) {
+  return *(const __attribute__((address_space(1))) V *)p;
+}
+__device__ __forceinline__ u32x4 ldg16(const void *p) { return ldg<u32x4>(p); }
+__device__ __forceinline__ float ldg_f32(const float *p) { return ldg<float>(p); }
+__device__ __forceinline__ uint2 ldg_u2(const void *p) {
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = ldg<u32x2>(p);
+  return uint2{v.x, v.y};
 }
 // Load bypassing the non-coherent per-CU cache (data written by other
 // workgroups of the same kernel).

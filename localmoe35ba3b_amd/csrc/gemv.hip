@@ -10,8 +10,16 @@
 
 namespace lm {
 
-constexpr int kGemvThreads = 256;
-constexpr int kGemvLoads = 8;
+constexpr int kGemvThreads = 256;  // workgroup size of the any-K kernels
+constexpr int kGemvLoads = 8;      // weight loads per lane at kGemvThreads
+// Large workgroups for launches that leave CUs idle or carry several
+// activation rows: four times more threads share a block's rows, so the
+// activation quantization, the weight loads of a lane (2 instead of 8) and
+// the dot products of each wave shrink by four, and four waves per SIMD hide
+// each other's dependency chains.  Launches of many blocks keep 256-thread
+// workgroups, several per CU, which keep more bytes in flight per CU.
+constexpr int kGemvThreadsK = 1024;
+static bool gemv_large_blocks(int64_t blocks, int mt) { return blocks < 256 || mt >= 4; }
 
 struct GemvArgs {
   const int64_t *table;  // grouped mode: [experts, 5] descriptor rows
@@ -74,11 +82,16 @@ __device__ __forceinline__ Resolved resolve(const GemvArgs &a) {
 
 // LDS carve-up: [xq or x16 | xs | ws | partials]
 // T: dtype of the activations (QUANT) and of the output.
-template <typename T, int MT, bool QUANT, bool PARTIALS>
-__global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
+// KC: the reduction length as a compile-time constant (the model's 2048 and
+// 512), or 0 for any K; with a constant K the load issue has no loops and
+// no branches, so every wait count stays exact.
+template <typename T, int MT, bool QUANT, bool PARTIALS, int KC, int TH>
+__global__ __launch_bounds__(TH) void w8a8_gemv_kernel(GemvArgs a) {
+  constexpr int LD = kGemvLoads * kGemvThreads / TH;  // weight loads per lane
+  static_assert(LD >= 1, "workgroup size");
   extern __shared__ __align__(16) unsigned char smem[];
   const Resolved rv = resolve(a);
-  const int K = a.K, G = K >> 7, M = a.M;
+  const int K = KC ? KC : a.K, G = K >> 7, M = a.M;
   int8_t *xq = reinterpret_cast<int8_t *>(smem);
   float *xs = reinterpret_cast<float *>(smem + MT * K);
   float *ws = xs + MT * G;
@@ -109,10 +122,11 @@ __global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
   // activations one register stage, the activations and scales are requested
   // first, the weights next, and the activations are staged in LDS only then,
   // so their wait does not include the weights: the two load latencies overlap.
-  constexpr int QJ = 2 * MT, XN = MT;
+  constexpr int QJ = 2 * MT * kGemvThreads / TH > 0 ? 2 * MT * kGemvThreads / TH : 1;
+  constexpr int XN = MT * kGemvThreads / TH > 0 ? MT * kGemvThreads / TH : 1;
   const int th = threadIdx.x;
-  if (rv.rvalid * G <= kGemvLoads * 8 * (kGemvThreads / 64) && M * G <= kGemvThreads &&
-      (QUANT ? M * G <= QJ * (kGemvThreads / 32) : M * K <= XN * 16 * kGemvThreads)) {
+  if (rv.rvalid * G <= LD * 8 * (TH / 64) && M * G <= TH &&
+      (QUANT ? M * G <= QJ * (TH / 32) : M * K <= XN * 16 * TH)) {
     QuantStage<T, QJ> qst;
     RowStage<XN> cst;
     if constexpr (QUANT)
@@ -120,17 +134,18 @@ __global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
     else
       cst.load(reinterpret_cast<const unsigned char *>(a.xq + (int64_t)rv.xrow * K), K, M, K);
     const int ti = min(th, M * G - 1);
-    const float xsv = (!QUANT && a.xs) ? a.xs[(int64_t)(rv.xrow + ti / G) * G + ti % G] : 0.0f;
+    const float xsv = (!QUANT && a.xs) ? ldg_f32(a.xs + (int64_t)(rv.xrow + ti / G) * G + ti % G) : 0.0f;
     const int tw = min(th, rv.rvalid * G - 1);
-    const float wsv = PARTIALS ? 0.0f : rv.s[(int64_t)rv.map(tw / G) * G + tw % G];
-    RowLoads<kGemvLoads, kGemvThreads> L;
+    const float wsv = PARTIALS ? 0.0f : ldg_f32(rv.s + (int64_t)rv.map(tw / G) * G + tw % G);
+    RowLoads<LD, TH> L;
     L.issue(rv.rvalid, G, row_ptr);
     if constexpr (QUANT)
       qst.store(K, xq, xs);
     else
       cst.store(reinterpret_cast<unsigned char *>(xq));
-    if (!QUANT && a.xs && th < M * G) xs[th] = xsv;
-    if (!PARTIALS && th < rv.rvalid * G) ws[th] = wsv;
+    // branch-free: surplus threads rewrite the last entry with its own value
+    if (!QUANT && a.xs) xs[ti] = xsv;
+    if (!PARTIALS) ws[tw] = wsv;
     __syncthreads();
     L.consume(body);
     __syncthreads();
@@ -151,7 +166,7 @@ __global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
     if constexpr (!PARTIALS) {
       for (int i = threadIdx.x; i < rv.rvalid * G; i += blockDim.x) {
         const int r = i / G, g = i - r * G;
-        ws[i] = rv.s[(int64_t)rv.map(r) * G + g];
+        ws[i] = ldg_f32(rv.s + (int64_t)rv.map(r) * G + g);
       }
     }
     __syncthreads();
@@ -190,11 +205,13 @@ __global__ __launch_bounds__(kGemvThreads) void w8a8_gemv_kernel(GemvArgs a) {
 
 // W8A16: dequantize to T exactly (T(q * s)), fp32 dot products.
 // LDS carve-up: [x16 rows | ws | partials]
-template <typename T, int MT>
-__global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_kernel(GemvArgs a) {
+template <typename T, int MT, int KC, int TH>
+__global__ __launch_bounds__(TH) void w8a16_gemv_kernel(GemvArgs a) {
+  constexpr int LD = kGemvLoads * kGemvThreads / TH;  // weight loads per lane
+  static_assert(LD >= 1, "workgroup size");
   extern __shared__ __align__(16) unsigned char smem[];
   const Resolved rv = resolve(a);
-  const int K = a.K, G = K >> 7, M = a.M;
+  const int K = KC ? KC : a.K, G = K >> 7, M = a.M;
   uint16_t *xl = reinterpret_cast<uint16_t *>(smem);
   float *ws = reinterpret_cast<float *>(smem + MT * K * 2);
   float *part = ws + a.RB * G;
@@ -226,17 +243,16 @@ __global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_kernel(GemvArgs a) {
   const unsigned char *xsrc = reinterpret_cast<const unsigned char *>(a.x + (int64_t)rv.xrow * a.ldx);
   // One batch, as in w8a8_gemv_kernel: activations and scales requested
   // before the weights, staged in LDS after them.
-  constexpr int XN = 2 * MT;
-  if (rv.rvalid * G <= kGemvLoads * 8 * (kGemvThreads / 64) &&
-      M * K * 2 <= XN * 16 * kGemvThreads) {
+  constexpr int XN = 2 * MT * kGemvThreads / TH > 0 ? 2 * MT * kGemvThreads / TH : 1;
+  if (rv.rvalid * G <= LD * 8 * (TH / 64) && M * K * 2 <= XN * 16 * TH) {
     RowStage<XN> cst;
     cst.load(xsrc, a.ldx * 2, M, K * 2);
     const int tw = min((int)threadIdx.x, rv.rvalid * G - 1);
-    const float wsv = rv.s[(int64_t)rv.map(tw / G) * G + tw % G];
-    RowLoads<kGemvLoads, kGemvThreads> L;
+    const float wsv = ldg_f32(rv.s + (int64_t)rv.map(tw / G) * G + tw % G);
+    RowLoads<LD, TH> L;
     L.issue(rv.rvalid, G, row_ptr);
     cst.store(reinterpret_cast<unsigned char *>(xl));
-    if ((int)threadIdx.x < rv.rvalid * G) ws[threadIdx.x] = wsv;
+    ws[tw] = wsv;  // branch-free: surplus threads rewrite the last entry with its own value
     __syncthreads();
     L.consume(body);
   } else {
@@ -246,7 +262,7 @@ __global__ __launch_bounds__(kGemvThreads) void w8a16_gemv_kernel(GemvArgs a) {
     }
     for (int i = threadIdx.x; i < rv.rvalid * G; i += blockDim.x) {
       const int r = i / G, g = i - r * G;
-      ws[i] = rv.s[(int64_t)rv.map(r) * G + g];
+      ws[i] = ldg_f32(rv.s + (int64_t)rv.map(r) * G + g);
     }
     __syncthreads();
     stream_rows<kGemvLoads>(rv.rvalid, G, row_ptr, body);
@@ -278,7 +294,22 @@ static int launch_w8a8(const GemvArgs &a, unsigned gy, hipStream_t st) {
                      (size_t)MT * a.RB * G * 4;
   LM_REQUIRE(lds <= 160 * 1024, LM_EINVAL, "Invalid INT8 group geometry");
   const unsigned gx = a.swiglu ? cdiv(a.N / 2, a.RB / 2) : cdiv(a.N, a.RB);
-  w8a8_gemv_kernel<T, MT, QUANT, PARTIALS><<<dim3(gx, gy), kGemvThreads, lds, st>>>(a);
+  const dim3 grid(gx, gy);
+  const bool large = gemv_large_blocks((int64_t)gx * gy, MT);
+  if (a.K == 2048 && large)
+    w8a8_gemv_kernel<T, MT, QUANT, PARTIALS, 2048, kGemvThreadsK>
+        <<<grid, kGemvThreadsK, lds, st>>>(a);
+  else if (a.K == 2048)
+    w8a8_gemv_kernel<T, MT, QUANT, PARTIALS, 2048, kGemvThreads>
+        <<<grid, kGemvThreads, lds, st>>>(a);
+  else if (a.K == 512 && large)
+    w8a8_gemv_kernel<T, MT, QUANT, PARTIALS, 512, kGemvThreadsK>
+        <<<grid, kGemvThreadsK, lds, st>>>(a);
+  else if (a.K == 512)
+    w8a8_gemv_kernel<T, MT, QUANT, PARTIALS, 512, kGemvThreads>
+        <<<grid, kGemvThreads, lds, st>>>(a);
+  else
+    w8a8_gemv_kernel<T, MT, QUANT, PARTIALS, 0, kGemvThreads><<<grid, kGemvThreads, lds, st>>>(a);
   return check_launch("w8a8_gemv_kernel");
 }
 
@@ -302,8 +333,18 @@ static int launch_w8a16(const GemvArgs &a, unsigned gy, hipStream_t st) {
   const int G = a.K / 128;
   const size_t lds = (size_t)MT * a.K * 2 + (size_t)a.RB * G * 4 + (size_t)MT * a.RB * G * 4;
   LM_REQUIRE(lds <= 160 * 1024, LM_EINVAL, "Invalid INT8 group geometry");
-  const unsigned gx = cdiv(a.N, a.RB);
-  w8a16_gemv_kernel<T, MT><<<dim3(gx, gy), kGemvThreads, lds, st>>>(a);
+  const dim3 grid(cdiv(a.N, a.RB), gy);
+  const bool large = gemv_large_blocks((int64_t)grid.x * gy, MT);
+  if (a.K == 2048 && large)
+    w8a16_gemv_kernel<T, MT, 2048, kGemvThreadsK><<<grid, kGemvThreadsK, lds, st>>>(a);
+  else if (a.K == 2048)
+    w8a16_gemv_kernel<T, MT, 2048, kGemvThreads><<<grid, kGemvThreads, lds, st>>>(a);
+  else if (a.K == 512 && large)
+    w8a16_gemv_kernel<T, MT, 512, kGemvThreadsK><<<grid, kGemvThreadsK, lds, st>>>(a);
+  else if (a.K == 512)
+    w8a16_gemv_kernel<T, MT, 512, kGemvThreads><<<grid, kGemvThreads, lds, st>>>(a);
+  else
+    w8a16_gemv_kernel<T, MT, 0, kGemvThreads><<<grid, kGemvThreads, lds, st>>>(a);
   return check_launch("w8a16_gemv_kernel");
 }
 

@@ -149,11 +149,14 @@ struct RowStage {
       v[u] = ldg16(src + m * pitch + c * 16);
     }
   }
+  // Branch-free as well: pieces past the end rewrite the last piece with the
+  // value it already holds (a store under a branch would make the compiler
+  // wait for every load in flight, the weights included).
   __device__ __forceinline__ void store(unsigned char *dst) const {
 #pragma unroll
     for (int u = 0; u < N; ++u) {
-      const int i = threadIdx.x + u * blockDim.x;
-      if (i < n) *reinterpret_cast<u32x4 *>(dst + (int64_t)i * 16) = v[u];
+      const int i = min((int)(threadIdx.x + u * blockDim.x), n - 1);
+      *reinterpret_cast<u32x4 *>(dst + (int64_t)i * 16) = v[u];
     }
   }
 };
@@ -169,9 +172,11 @@ __device__ __forceinline__ float halfwave_max(float a) {
 }
 
 // Quantizes one 128-group (4 values per lane of a half-wave, w8a8.py:8-14)
-// into xq[g * 128 + 4 l ..] and, from lane 0, its scale; `store` guards both.
+// into xq[g * 128 + 4 l ..] and, from lane 0, its scale.  Callers pass the
+// destination of a real job; surplus lanes redo the last job and store the
+// same bytes to it again, so no store is under a branch.
 template <typename T>
-__device__ __forceinline__ void quantize_group(uint2 raw, int l, bool store, int8_t *xq_group,
+__device__ __forceinline__ void quantize_group(uint2 raw, int l, int8_t *xq_group,
                                                float *xs_slot) {
   const float inv127 = (float)(1.0 / 127.0);
   float v[4] = {T::to_f32(raw.x & 0xFFFFu), T::to_f32(raw.x >> 16), T::to_f32(raw.y & 0xFFFFu),
@@ -183,10 +188,8 @@ __device__ __forceinline__ void quantize_group(uint2 raw, int l, bool store, int
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[i] / sc)) << (8 * i);
-  if (store) {
-    *reinterpret_cast<uint32_t *>(xq_group + l * 4) = packed;
-    if (l == 0) *xs_slot = sc;
-  }
+  *reinterpret_cast<uint32_t *>(xq_group + l * 4) = packed;
+  if (l == 0) *xs_slot = sc;
 }
 
 // QuantStage: a half-wave owns (row, group) jobs half, half + nhalf, ... (at
@@ -203,17 +206,16 @@ struct QuantStage {
     for (int u = 0; u < J; ++u) {
       const int job = min(half + u * nhalf, jobs - 1);
       const int m = job / G, g = job - (job / G) * G;
-      raw[u] = *reinterpret_cast<const uint2 *>(x + m * ldx + g * 128 + l * 4);
+      raw[u] = ldg_u2(x + m * ldx + g * 128 + l * 4);
     }
   }
   __device__ __forceinline__ void store(int K, int8_t *xq, float *xs) const {
     const int half = threadIdx.x >> 5, nhalf = blockDim.x >> 5, l = threadIdx.x & 31;
 #pragma unroll
     for (int u = 0; u < J; ++u) {
-      const int jr = half + u * nhalf;
-      const int job = min(jr, jobs - 1);
+      const int job = min(half + u * nhalf, jobs - 1);
       const int m = job / G, g = job - (job / G) * G;
-      quantize_group<T>(raw[u], l, jr < jobs, xq + m * K + g * 128, xs + m * G + g);
+      quantize_group<T>(raw[u], l, xq + m * K + g * 128, xs + m * G + g);
     }
   }
 };
@@ -241,14 +243,13 @@ __device__ __forceinline__ void quantize_rows_to_lds(const uint16_t *x, int64_t 
     for (int u = 0; u < B; ++u) {
       const int job = min(base + u * nhalf, jobs - 1);
       const int m = job / G, g = job - (job / G) * G;
-      raw[u] = *reinterpret_cast<const uint2 *>(x + m * ldx + g * 128 + l * 4);
+      raw[u] = ldg_u2(x + m * ldx + g * 128 + l * 4);
     }
 #pragma unroll
     for (int u = 0; u < B; ++u) {
-      const int jr = base + u * nhalf;
-      const int job = min(jr, jobs - 1);
+      const int job = min(base + u * nhalf, jobs - 1);
       const int m = job / G, g = job - (job / G) * G;
-      quantize_group<T>(raw[u], l, jr < jobs, xq + m * K + g * 128, xs + m * G + g);
+      quantize_group<T>(raw[u], l, xq + m * K + g * 128, xs + m * G + g);
     }
   }
 }

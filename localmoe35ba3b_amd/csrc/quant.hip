@@ -49,8 +49,9 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t *__restri
                                                         float *__restrict__ s,
                                                         int64_t ngroups) {
   // A half-wave quantizes B groups per pass: all B loads are issued before
-  // the first is used and the groups are computed branch-free (only the
-  // stores are guarded), so a pass costs one load latency.
+  // the first is used and the groups are computed branch-free (slots past
+  // the end redo the last group and store the same bytes to it again), so a
+  // pass costs one load latency.
   constexpr int B = 4;
   const int l = threadIdx.x & 31;
   const int64_t half = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 5;
@@ -64,9 +65,8 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t *__restri
     }
 #pragma unroll
     for (int u = 0; u < B; ++u) {
-      const int64_t gr = base + u * nhalf;
-      const int64_t grp = min(gr, ngroups - 1);
-      quantize_group<T>(raw[u], l, gr < ngroups, q + grp * 128, s + grp);
+      const int64_t grp = min(base + u * nhalf, ngroups - 1);
+      quantize_group<T>(raw[u], l, q + grp * 128, s + grp);
     }
   }
 }
