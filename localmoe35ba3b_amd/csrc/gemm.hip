@@ -468,11 +468,18 @@ __device__ __forceinline__ void barrier_raw() { asm volatile("s_barrier" ::: "me
 // current one (one MFMA, then a few VALU ops), so a wave keeps the matrix
 // pipe and the VALU busy together.
 //
-// K order inside a 64-K stage: lane l (quad q = l >> 4) loads 16 consecutive
-// weights k = 16 q .. 16 q + 15 of its column; MFMA step `sub` takes the
-// half 8 sub .. 8 sub + 7.  The A fragment of the same lane and step reads
-// the same k from LDS, so each product pairs the right x and w (a fixed
-// permutation of the summation order inside the stage).
+// K order inside a 64-K stage: in the MFMA layout lane l (quarter q = l >> 4)
+// holds 16 consecutive weights k = 16 q .. 16 q + 15 of column l & 15; MFMA
+// step `sub` takes the half 8 sub .. 8 sub + 7.  The A fragment of the same
+// lane and step reads the same k from LDS, so each product pairs the right x
+// and w (a fixed permutation of the summation order inside the stage).
+//
+// The weights are not loaded in that layout: there a quarter-wave touches 16
+// rows 2 KB apart, which keeps the address path busy with 16 cache lines per
+// quarter-wave.  Instead quarter-wave a loads 64 contiguous bytes of each of
+// rows 4 a .. 4 a + 3 (lane 16 a + 4 b + p: row 4 a + b, piece p), 4 lines
+// per quarter-wave, and one ds_bpermute per dword moves piece p of row r to
+// lane 16 p + r while the previous stage's MFMAs run.
 //
 // A stage in LDS: BM rows x 128 B (64 bf16); 16-byte chunk p of row r is
 // stored at chunk p ^ rb_swz(r).  Scales of the tile are staged once,
@@ -489,8 +496,8 @@ __device__ __forceinline__ int rb_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); 
 // MS so the inner loop carries no row branches; every load is unconditional
 // (rows past the tile re-read its last row), which keeps the compiler's
 // wait counts exact.  A stage is KS = 64 HL values of K: each lane loads HL
-// 16-byte pieces per column sub-tile (bytes 64 h + 16 q, h < HL), so one
-// lane quad reads 64 HL contiguous bytes of a weight row.  Weights are
+// 16-byte pieces per column sub-tile (bytes 64 h + 16 p, h < HL), so four
+// consecutive lanes read 64 contiguous bytes of a weight row.  Weights are
 // requested BD - 1 stages ahead, activation rows AD stages ahead (AD - 1
 // stages wait in registers, one more in LDS).
 template <typename T, bool SWIGLU, bool GATHER, int K, int BM, int TN, int BD, int HL, int AD, int NW,
@@ -553,12 +560,13 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
     const int wr = wrow(piece / (G / 4));
     sreg[j] = ldg16(wsc + (int64_t)(wr >= 0 ? wr : 0) * G + (piece % (G / 4)) * 4);
   }
-  // Weight sources: column col_base(ni) + (lane & 15), bytes 16 q (+ 64 h) of each stage.
+  // Weight sources: lane 16 a + 4 b + p loads column col_base(ni) + 4 a + b,
+  // bytes 16 p (+ 64 h) of each stage; rb_perm moves them into the MFMA layout.
   const int8_t *bsrc[NI];
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    const int wr = wrow(col_base(ni) + (lane & 15));
-    bsrc[ni] = wq + (int64_t)(wr >= 0 ? wr : 0) * K + q * 16;
+    const int wr = wrow(col_base(ni) + 4 * q + ((lane & 15) >> 2));
+    bsrc[ni] = wq + (int64_t)(wr >= 0 ? wr : 0) * K + (lane & 3) * 16;
   }
   // Activation sources: wave-load j fills rows RPL (4 j + wave) ..; lane ->
   // row RPL (4 j + wave) + lane / CPR, LDS chunk lane % CPR, which holds the
@@ -574,6 +582,19 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
 
   u32x4 breg[BD][NI][HL];
   u32x4 areg[AS][A_W];
+  // Lane 16 p + r takes piece p of row r from lane 16 (r >> 2) + 4 (r & 3) + p
+  // (a byte address for ds_bpermute).
+  const int perm_src = 4 * (16 * ((lane & 15) >> 2) + 4 * (lane & 3) + q);
+  auto rb_perm = [&](int slot) {
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+      for (int h = 0; h < HL; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          breg[slot][ni][h][j] =
+              (uint32_t)__builtin_amdgcn_ds_bpermute(perm_src, (int)breg[slot][ni][h][j]);
+  };
   auto load_b = [&](int slot, int s) {
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni)
@@ -639,6 +660,7 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   u32x4 bcur[NI];
   __builtin_amdgcn_s_waitcnt(0xC07F);
   barrier_raw();
+  rb_perm(0);
   dq(0, 0, 0, bcur);
   constexpr int VG = (20 * NI + MS * NI - 1) / (MS * NI);  // dequant VALU per MFMA
   auto step = [&](int s, int ub, int ua, bool st_a, bool ld_a, bool ld_b, bool has_next) {
@@ -659,6 +681,9 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
             sa + r * ROWB + (((8 * (p >> 1) + 2 * q + (p & 1)) ^ rb_swz(r)) * 16));
       }
       const bool nxt = p + 1 < P || has_next;
+      // The next stage's weights are moved into the MFMA layout during this
+      // stage's first piece, one piece before their first dequantization.
+      if (p == 0 && has_next) rb_perm((ub + 1) % BD);
       u32x4 bn[NI];
       if (p + 1 < P)
         dq(ub, s, p + 1, bn);
