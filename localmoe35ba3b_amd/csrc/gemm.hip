@@ -474,12 +474,14 @@ __device__ __forceinline__ void barrier_raw() { asm volatile("s_barrier" ::: "me
 // lane and step reads the same k from LDS, so each product pairs the right x
 // and w (a fixed permutation of the summation order inside the stage).
 //
-// The weights are not loaded in that layout: there a quarter-wave touches 16
-// rows 2 KB apart, which keeps the address path busy with 16 cache lines per
-// quarter-wave.  Instead quarter-wave a loads 64 contiguous bytes of each of
-// rows 4 a .. 4 a + 3 (lane 16 a + 4 b + p: row 4 a + b, piece p), 4 lines
+// Streamed weights (RP = true: the routed GEMMs, which read each expert's
+// weights once) are not loaded in that layout: there a quarter-wave touches
+// 16 rows 2 KB apart, which keeps the address path busy with 16 cache lines
+// per quarter-wave.  Instead quarter-wave a loads 64 contiguous bytes of each
+// of rows 4 a .. 4 a + 3 (lane 16 a + 4 b + p: row 4 a + b, piece p), 4 lines
 // per quarter-wave, and one ds_bpermute per dword moves piece p of row r to
-// lane 16 p + r while the previous stage's MFMAs run.
+// lane 16 p + r while the previous stage's MFMAs run.  Dense weights, which
+// every row tile re-reads from cache, are loaded in the MFMA layout directly.
 //
 // A stage in LDS: BM rows x 128 B (64 bf16); 16-byte chunk p of row r is
 // stored at chunk p ^ rb_swz(r).  Scales of the tile are staged once,
@@ -500,8 +502,8 @@ __device__ __forceinline__ int rb_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); 
 // consecutive lanes read 64 contiguous bytes of a weight row.  Weights are
 // requested BD - 1 stages ahead, activation rows AD stages ahead (AD - 1
 // stages wait in registers, one more in LDS).
-template <typename T, bool SWIGLU, bool GATHER, int K, int BM, int TN, int BD, int HL, int AD, int NW,
-          int MS>
+template <typename T, bool SWIGLU, bool GATHER, bool RP, int K, int BM, int TN, int BD, int HL, int AD,
+          int NW, int MS>
 __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t start, int rows,
                                         int nt, unsigned char *smem) {
   constexpr int KS = 64 * HL;
@@ -560,13 +562,15 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
     const int wr = wrow(piece / (G / 4));
     sreg[j] = ldg16(wsc + (int64_t)(wr >= 0 ? wr : 0) * G + (piece % (G / 4)) * 4);
   }
-  // Weight sources: lane 16 a + 4 b + p loads column col_base(ni) + 4 a + b,
-  // bytes 16 p (+ 64 h) of each stage; rb_perm moves them into the MFMA layout.
+  // Weight sources, bytes (+ 64 h) of each stage: with RP, lane 16 a + 4 b + p
+  // loads column col_base(ni) + 4 a + b, bytes 16 p, and rb_perm moves them into
+  // the MFMA layout; otherwise lane l loads column col_base(ni) + (l & 15),
+  // bytes 16 q.
   const int8_t *bsrc[NI];
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    const int wr = wrow(col_base(ni) + 4 * q + ((lane & 15) >> 2));
-    bsrc[ni] = wq + (int64_t)(wr >= 0 ? wr : 0) * K + (lane & 3) * 16;
+    const int wr = wrow(col_base(ni) + (RP ? 4 * q + ((lane & 15) >> 2) : lane & 15));
+    bsrc[ni] = wq + (int64_t)(wr >= 0 ? wr : 0) * K + (RP ? lane & 3 : q) * 16;
   }
   // Activation sources: wave-load j fills rows RPL (4 j + wave) ..; lane ->
   // row RPL (4 j + wave) + lane / CPR, LDS chunk lane % CPR, which holds the
@@ -586,14 +590,16 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   // (a byte address for ds_bpermute).
   const int perm_src = 4 * (16 * ((lane & 15) >> 2) + 4 * (lane & 3) + q);
   auto rb_perm = [&](int slot) {
+    if constexpr (RP) {
 #pragma unroll
-    for (int ni = 0; ni < NI; ++ni)
+      for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
-      for (int h = 0; h < HL; ++h)
+        for (int h = 0; h < HL; ++h)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          breg[slot][ni][h][j] =
-              (uint32_t)__builtin_amdgcn_ds_bpermute(perm_src, (int)breg[slot][ni][h][j]);
+          for (int j = 0; j < 4; ++j)
+            breg[slot][ni][h][j] =
+                (uint32_t)__builtin_amdgcn_ds_bpermute(perm_src, (int)breg[slot][ni][h][j]);
+    }
   };
   auto load_b = [&](int slot, int s) {
 #pragma unroll
@@ -752,8 +758,8 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   }
 }
 
-template <typename T, bool SWIGLU, bool GATHER, int K, int BM, int TN, int BD, int HL, int AD,
-          int NW, int OCC>
+template <typename T, bool SWIGLU, bool GATHER, bool RP, int K, int BM, int TN, int BD, int HL,
+          int AD, int NW, int OCC>
 __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
   constexpr int SC_BYTES = NW * TN * (K / 128) * 4;
   __shared__ __align__(16) unsigned char smem[3 * BM * 128 * HL + SC_BYTES];
@@ -774,13 +780,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
   if (rows <= 0) return;
   static_assert(BM == 96, "row-count dispatch below covers 96-row tiles");
   if (rows > 80)
-    rb_tile<T, SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 6>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, RP, K, BM, TN, BD, HL, AD, NW, 6>(a, e, start, rows, nt, smem);
   else if (rows > 64)
-    rb_tile<T, SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 5>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, RP, K, BM, TN, BD, HL, AD, NW, 5>(a, e, start, rows, nt, smem);
   else if (rows > 32)
-    rb_tile<T, SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 4>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, RP, K, BM, TN, BD, HL, AD, NW, 4>(a, e, start, rows, nt, smem);
   else
-    rb_tile<T, SWIGLU, GATHER, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, RP, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem);
 }
 
 // Configuration of grouped_rb_kernel, chosen by measurement on the
@@ -795,7 +801,9 @@ constexpr int kRbAD = 2;
 constexpr int kRbNW = 4;
 constexpr int kGroupedBN = 128;  // grouped_mfma_kernel tile columns
 
-template <typename T, bool SWIGLU, bool GATHER>
+// RP: reassigned weight loads + permute (weights streamed once, the routed
+// GEMMs); dense weights are loaded in the MFMA layout directly.
+template <typename T, bool SWIGLU, bool GATHER, bool RP>
 static int launch_grouped(GemmArgs a, unsigned mtiles, hipStream_t st) {
   if (mtiles == 0) return LM_OK;
   if (a.tile_rows <= 96 && (a.K == 2048 || a.K == 512)) {
@@ -805,10 +813,10 @@ static int launch_grouped(GemmArgs a, unsigned mtiles, hipStream_t st) {
     const int64_t grid = xcd_grid(a.mt_count, a.nt_count);
     LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
     if (a.K == 2048)
-      grouped_rb_kernel<T, SWIGLU, GATHER, 2048, 96, kRbTN, kRbBD, kRbHL, kRbAD, kRbNW, kRbOcc>
+      grouped_rb_kernel<T, SWIGLU, GATHER, RP, 2048, 96, kRbTN, kRbBD, kRbHL, kRbAD, kRbNW, kRbOcc>
           <<<(unsigned)grid, kRbNW * 64, 0, st>>>(a);
     else
-      grouped_rb_kernel<T, SWIGLU, GATHER, 512, 96, kRbTN, kRbBD, kRbHL, kRbAD, kRbNW, kRbOcc>
+      grouped_rb_kernel<T, SWIGLU, GATHER, RP, 512, 96, kRbTN, kRbBD, kRbHL, kRbAD, kRbNW, kRbOcc>
           <<<(unsigned)grid, kRbNW * 64, 0, st>>>(a);
     return check_launch("grouped_rb_kernel");
   }
@@ -851,8 +859,8 @@ int w8a16_gemm_dense(const void *x, const int8_t *q, const float *s, void *y, in
   // because each wave dequantizes only its own columns' weights.
   if (k == 2048 || k == 512) {
     a.tile_rows = 96;
-    return dtype == LM_BF16 ? launch_grouped<BF16, false, false>(a, cdiv(m, 96), st)
-                            : launch_grouped<FP16, false, false>(a, cdiv(m, 96), st);
+    return dtype == LM_BF16 ? launch_grouped<BF16, false, false, false>(a, cdiv(m, 96), st)
+                            : launch_grouped<FP16, false, false, false>(a, cdiv(m, 96), st);
   }
   const unsigned mt = cdiv(m, 128);
   if (dtype == LM_BF16) return launch_gemm<BF16, 128, 2, false, false, true>(a, mt, st);
@@ -863,10 +871,10 @@ template <typename T>
 static int routed_dispatch(const GemmArgs &a, unsigned mt, bool gather, bool swiglu,
                            hipStream_t st) {
   if (swiglu)
-    return gather ? launch_grouped<T, true, true>(a, mt, st)
-                  : launch_grouped<T, true, false>(a, mt, st);
-  return gather ? launch_grouped<T, false, true>(a, mt, st)
-                : launch_grouped<T, false, false>(a, mt, st);
+    return gather ? launch_grouped<T, true, true, true>(a, mt, st)
+                  : launch_grouped<T, true, false, true>(a, mt, st);
+  return gather ? launch_grouped<T, false, true, true>(a, mt, st)
+                : launch_grouped<T, false, false, true>(a, mt, st);
 }
 
 int routed_gemm(const RoutedGemm &r, hipStream_t st) {
