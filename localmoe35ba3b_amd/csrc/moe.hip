@@ -66,7 +66,7 @@ constexpr WsLayout layout(int64_t T) {
   w.xs = take(kH / 128 * 4);
   w.pos = take((R + T) * 8);
   w.table = take(w.n_tiles * 3 * 8);
-  w.bcounts = take((T + kTopkTokens - 1) / kTopkTokens * kE * 4);  // per top-k workgroup expert counts
+  w.bcounts = take((T + kTopkTokens - 1) / kTopkTokens * kE);  // per top-k workgroup expert counts (bytes)
   w.rslot = take(R * 4);  // rank of each route inside its top-k workgroup and expert
   w.rpos = take(R * 4);   // sorted row of each route
   w.hbuf = take((R + T) * kI * 2);
@@ -873,7 +873,7 @@ constexpr int kScanGroups = kScanRoutes / (kTopkTokens * kTopK);  // top-k workg
 static_assert(kScanGroups * kTopkTokens * kTopK == kScanRoutes, "scan slices whole top-k groups");
 
 __global__ __launch_bounds__(kTopkTokens * 64) void prefill_topk_count_kernel(LayerArgs a, int T,
-                                                                             int *bcounts,
+                                                                             uint8_t *bcounts,
                                                                              int *rslot) {
   __shared__ int lcnt[kE];
   __shared__ int64_t sid[kTopkTokens][kTopK];
@@ -903,26 +903,32 @@ __global__ __launch_bounds__(kTopkTokens * 64) void prefill_topk_count_kernel(La
     }
   }
   __syncthreads();
-  if (t < kE) bcounts[(int64_t)blockIdx.x * kE + t] = lcnt[t];
+  // a count is at most kTopkTokens * kTopK = 64 routes: one byte
+  if (t < kE) bcounts[(int64_t)blockIdx.x * kE + t] = (uint8_t)lcnt[t];
   if (e >= 0) rslot[(int64_t)tok * kTopK + lane] = rank;
 }
 
 // Expert offsets and, for each route, its row in the expert-sorted order:
 // offs[e] + (routes to e of earlier top-k workgroups) + rank inside its own
 // workgroup.  Each workgroup handles kScanRoutes routes and sums the bcounts
-// columns itself (nb rows, L2-resident), so no grid-wide step is needed.
-// Workgroup 0 also writes the tile table (kBM-row tiles per expert, surplus
-// rows (0, 0, 0), then the shared expert's tiles over rows [R, R + T)) and
-// the shared rows' tokens.
+// columns itself (nb rows of kE byte counts, 64 KB for 2048 tokens), so no
+// grid-wide step is needed.  Workgroup 0 also writes the tile table (kBM-row
+// tiles per expert, surplus rows (0, 0, 0), then the shared expert's tiles
+// over rows [R, R + T)) and the shared rows' tokens.
+//
+// Every load of a phase is issued unconditionally (clamped rows), so the
+// phase pays one load latency, not one per row.
 __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__restrict__ ids,
                                                             const int *__restrict__ rslot,
-                                                            const int *__restrict__ bcounts,
+                                                            const uint8_t *__restrict__ bcounts,
                                                             int nb, int T, int max_tiles,
                                                             int64_t *__restrict__ pos,
                                                             int64_t *__restrict__ table,
                                                             int *__restrict__ rpos) {
-  __shared__ int ptot[4][kE], ppre[4][kE], bpre[kScanGroups][kE];
-  __shared__ int offs[kE + 1], tends[kE], scratch[4];
+  constexpr int Q = 16;  // row phases: wave q sums rows q, q + Q, ...
+  static_assert(kE == 4 * 64, "a lane sums 4 experts' byte counts");
+  __shared__ int ptot[Q][kE], ppre[Q][kE], bpre[kScanGroups][kE];
+  __shared__ int offs[kE + 1], scratch[4];
   const int t = threadIdx.x;
   const int R = T * kTopK;
   const int r = blockIdx.x * kScanRoutes + t;
@@ -930,26 +936,39 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
   const int s_r = r < R ? rslot[r] : 0;
   const int j0 = blockIdx.x * kScanGroups;
   {
-    const int e = t & (kE - 1), q = t >> 8;
-    int tot = 0, pre = 0;
+    const int l = t & 63, q = t >> 6;
+    int tot[4] = {0, 0, 0, 0}, pre[4] = {0, 0, 0, 0};
 #pragma unroll 16
-    for (int j = q; j < nb; j += 4) {
-      const int c = bcounts[(int64_t)j * kE + e];
-      tot += c;
-      pre += j < j0 ? c : 0;
+    for (int j = q; j < nb; j += Q) {
+      const uint32_t v = *reinterpret_cast<const uint32_t *>(bcounts + (int64_t)j * kE + 4 * l);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = (int)((v >> (8 * i)) & 0xFFu);
+        tot[i] += c;
+        pre[i] += j < j0 ? c : 0;
+      }
     }
-    ptot[q][e] = tot;
-    ppre[q][e] = pre;
+    *reinterpret_cast<int4 *>(&ptot[q][4 * l]) = int4{tot[0], tot[1], tot[2], tot[3]};
+    *reinterpret_cast<int4 *>(&ppre[q][4 * l]) = int4{pre[0], pre[1], pre[2], pre[3]};
   }
+  // this workgroup's own kScanGroups rows, requested before the barrier
+  int cj[kScanGroups];
+#pragma unroll
+  for (int j = 0; j < kScanGroups; ++j)
+    cj[j] = bcounts[(int64_t)min(j0 + j, nb - 1) * kE + (t & (kE - 1))];
   __syncthreads();
   int c = 0;
   if (t < kE) {
-    c = ptot[0][t] + ptot[1][t] + ptot[2][t] + ptot[3][t];
-    int p = ppre[0][t] + ppre[1][t] + ppre[2][t] + ppre[3][t];
+    int p = 0;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      c += ptot[q][t];
+      p += ppre[q][t];
+    }
 #pragma unroll
     for (int j = 0; j < kScanGroups; ++j) {
       bpre[j][t] = p;
-      p += (j0 + j < nb) ? bcounts[(int64_t)(j0 + j) * kE + t] : 0;
+      p += (j0 + j < nb) ? cj[j] : 0;
     }
   }
   auto scan = [&](int v, int *total) {
@@ -980,28 +999,21 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
     rpos[r] = p;
   }
   if (blockIdx.x != 0) return;
+  // Tile table: thread e writes the tiles of expert e at its exclusive tile
+  // prefix; rows past the last tile up to max_tiles are (0, 0, 0).
   const int nt = t < kE ? (c + kBM - 1) / kBM : 0;
   int ntot = 0;
   const int tex = scan(nt, &ntot);
-  if (t < kE) tends[t] = tex + nt;
-  __syncthreads();
-  for (int i = t; i < max_tiles; i += 1024) {
-    int64_t te = 0, ts = 0, tp = 0;
-    if (i < ntot) {
-      int l = 0, h = kE;
-      while (l < h) {
-        const int mid = (l + h) >> 1;
-        if (tends[mid] <= i) l = mid + 1;
-        else h = mid;
-      }
-      const int prior = l > 0 ? tends[l - 1] : 0;
-      te = l;
-      ts = offs[l] + (int64_t)(i - prior) * kBM;
-      tp = offs[l + 1];
-    }
-    table[i * 3] = te;
-    table[i * 3 + 1] = ts;
-    table[i * 3 + 2] = tp;
+  for (int k = 0; k < nt; ++k) {
+    const int64_t i = tex + k;
+    table[i * 3] = t;
+    table[i * 3 + 1] = offs[t] + (int64_t)k * kBM;
+    table[i * 3 + 2] = offs[t + 1];
+  }
+  for (int i = ntot + t; i < max_tiles; i += 1024) {
+    table[(int64_t)i * 3] = 0;
+    table[(int64_t)i * 3 + 1] = 0;
+    table[(int64_t)i * 3 + 2] = 0;
   }
   const int nst = (T + kBM - 1) / kBM;
   for (int j = t; j < nst; j += 1024) {
@@ -1231,7 +1243,7 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   const int64_t T = tokens, R = T * kTopK;
   int64_t *pos = reinterpret_cast<int64_t *>(ws + w.pos);
   int64_t *table = reinterpret_cast<int64_t *>(ws + w.table);
-  int *bcounts = reinterpret_cast<int *>(ws + w.bcounts);
+  uint8_t *bcounts = ws + w.bcounts;
   int *rslot = reinterpret_cast<int *>(ws + w.rslot);
   int *rpos = reinterpret_cast<int *>(ws + w.rpos);
   uint16_t *vbuf = reinterpret_cast<uint16_t *>(ws + w.vbuf);
