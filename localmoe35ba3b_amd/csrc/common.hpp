@@ -280,6 +280,18 @@ __device__ __forceinline__ float row_sum_f32(float v) {
   return v;
 }
 
+// x / s for the W8A8 activation quantization (w8a8.py:8-14), given
+// r = 1 / s correctly rounded (one division per 128-group): one multiply and
+// Markstein's fused correction step.  For every bf16 and fp16 value x with
+// |x| <= the group absmax that s is formed from, rint of the result equals
+// rint of the correctly rounded quotient (tests/native/test_quant_division.c
+// checks all 2.07e9 such pairs), so the int8 values are the reference's.
+__device__ __forceinline__ float quant_div(float x, float s, float r) {
+  const float y = x * r;
+  const float e = __builtin_fmaf(-y, s, x);
+  return __builtin_fmaf(e, r, y);
+}
+
 // ------------------------------------------------------------ wave selection
 // Lane l's copy of lane l ^ D's value (D = 1, 2, 4, 8, 16, 32): quad
 // permutations for 1 and 2, the two row shifts by 4 written into alternate

@@ -162,13 +162,17 @@ struct RowStage {
 };
 
 // Absmax of a 128-group held as 4 values per lane by one half-wave: four DPP
-// steps inside each 16-lane row, one shuffle across the half-wave's two rows.
+// steps inside each 16-lane row, then v_permlane16_swap, which exchanges the
+// two rows of each row pair (both results hold one row each, so their max is
+// the pair's max whichever way round they come back).  All VALU: no LDS
+// counter wait, so the groups of several jobs interleave.
 __device__ __forceinline__ float halfwave_max(float a) {
   a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0xB1, 0xF, 0xF, false)));
   a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x4E, 0xF, 0xF, false)));
   a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x141, 0xF, 0xF, false)));
   a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x140, 0xF, 0xF, false)));
-  return fmaxf(a, __shfl_xor(a, 16, 64));
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 
 // Quantizes one 128-group (4 values per lane of a half-wave, w8a8.py:8-14)
@@ -184,10 +188,11 @@ __device__ __forceinline__ void quantize_group(uint2 raw, int l, int8_t *xq_grou
   const float a =
       halfwave_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
   const float sc = fmaxf(a, 1e-10f) * inv127;
+  const float r = 1.0f / sc;
   uint32_t packed = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[i] / sc)) << (8 * i);
+    packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(quant_div(v[i], sc, r))) << (8 * i);
   *reinterpret_cast<uint32_t *>(xq_group + l * 4) = packed;
   if (l == 0) *xs_slot = sc;
 }

@@ -186,14 +186,14 @@ __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
       float v[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[j] = xf[g * 128 + l * 4 + j];
-      float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+      const float am =
+          halfwave_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
       const float sc = fmaxf(am, 1e-10f) * (float)(1.0 / 127.0);
+      const float rs = 1.0f / sc;
       uint32_t packed = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[j] / sc)) << (8 * j);
+        packed |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(quant_div(v[j], sc, rs))) << (8 * j);
       *reinterpret_cast<uint32_t *>(a.xq + g * 128 + l * 4) = packed;
       if (l == 0) a.xs[g] = sc;
     }
@@ -488,17 +488,18 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   float am = 0.0f;
 #pragma unroll
   for (int j = 0; j < 16; ++j) am = fmaxf(am, fabsf(v[j]));
-  am = fmaxf(am, __shfl_xor(am, 1, 64));
-  am = fmaxf(am, __shfl_xor(am, 2, 64));
-  am = fmaxf(am, __shfl_xor(am, 4, 64));
+  am = fmaxf(am, __uint_as_float(lane_xor<1>(__float_as_uint(am))));
+  am = fmaxf(am, __uint_as_float(lane_xor<2>(__float_as_uint(am))));
+  am = fmaxf(am, __uint_as_float(lane_xor<4>(__float_as_uint(am))));
   const float sc = fmaxf(am, 1e-10f) * (float)(1.0 / 127.0);
+  const float rs = 1.0f / sc;
   u32x4 packed;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     uint32_t pk = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      pk |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(v[4 * j + i] / sc)) << (8 * i);
+      pk |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(quant_div(v[4 * j + i], sc, rs))) << (8 * i);
     packed[j] = pk;
   }
   *reinterpret_cast<u32x4 *>(xq + row * kI + col) = packed;
