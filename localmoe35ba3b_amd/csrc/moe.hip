@@ -425,12 +425,14 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   constexpr int RR = kTopK * kDnCols;  // routed rows
   constexpr int R = RR + kDnCols;      // + the shared expert's
   static_assert(RR * G == 256, "one routed group scale per thread");
+  static_assert(RR == 64, "the epilogue's per-slot terms fill wave 0");
   __shared__ __align__(16) int8_t xq[kTopK * kI];
   __shared__ float xs[kTopK * G];
   __shared__ __align__(16) uint16_t xsh[kI];
   __shared__ float term[R * G];
   __shared__ float wsc[R * G];
   __shared__ float selw[kTopK];
+  __shared__ float prod[RR];
   const int t = threadIdx.x;
   // Workgroup b runs on XCD b % 8; column tiles are dealt out so that the 8
   // workgroups writing one 128-byte line of h (64 columns) share an XCD.
@@ -443,13 +445,19 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   // Every load is issued by every thread from a valid address (only the
   // stores are guarded): a load inside a branch makes the compiler wait for
   // all loads in flight where the branch joins.  Loads complete in issue
-  // order, so the routed SwiGLU rows (quantized while the weights stream)
-  // come first, then the routed scales and weights, and last the shared
-  // expert's inputs, which are used after the routed rows.
+  // order, so the SwiGLU rows (quantized while the weights stream) and the
+  // other small inputs that do not depend on the ids come first, then the
+  // routed scales and weights, and last the shared expert's weights.
   const int row = t >> 5, col = (t & 31) * 16;
   const u32x4 h0 = ldg16(a.hbuf + row * kI + col);
   const u32x4 h1 = ldg16(a.hbuf + row * kI + col + 8);
   const float wsel = a.selw[t & (kTopK - 1)];
+  const u32x4 hsh = ldg16(a.hbuf + kTopK * kI + (t & (kI / 8 - 1)) * 8);
+  const int fs = t & (kDnCols * G - 1);
+  const float ssv = a.dn_s[(int64_t)kE * a.dn_ses + (int64_t)(c0 + fs / G) * G + fs % G];
+  const uint16_t hres = a.h[c0 + (t & (kDnCols - 1))];
+  const float glv = a.gl[0];
+  __builtin_amdgcn_sched_barrier(0);  // the inputs above are requested before the weights
   // Routed pairs f = row * G + group: wave w owns pairs 64 w .. 64 w + 63,
   // i.e. the rows of slots 2 w and 2 w + 1, and thread f loads the scale of
   // pair f.
@@ -468,11 +476,6 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   Ls.issue(kDnCols, G, [&](int r) {
     return a.dn_q + (int64_t)kE * a.dn_qes + (int64_t)(c0 + r) * kI;
   });
-  const int fs = t & (kDnCols * G - 1);
-  const float ssv = a.dn_s[(int64_t)kE * a.dn_ses + (int64_t)(c0 + fs / G) * G + fs % G];
-  const u32x4 hsh = ldg16(a.hbuf + kTopK * kI + (t & (kI / 8 - 1)) * 8);
-  const uint16_t hres = a.h[c0 + (t & (kDnCols - 1))];
-  const float glv = a.gl[0];
   __builtin_amdgcn_sched_barrier(0);  // keep the quantization below the weight loads
 
   // Row quantization of hbuf[0..7]: 16 values per thread, a 128-group is
@@ -505,6 +508,8 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   *reinterpret_cast<u32x4 *>(xq + row * kI + col) = packed;
   if ((t & 7) == 0) xs[row * G + col / 128] = sc;
   if (t < kTopK) selw[t] = wsel;
+  if (t < kDnCols * G) wsc[RR * G + t] = ssv;
+  if (t < kI / 8) reinterpret_cast<u32x4 *>(xsh)[t] = hsh;
   __syncthreads();
 
   // The routed scales of the pairs a wave consumes are the ones its own
@@ -519,9 +524,6 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
         dot16_i8(w, *reinterpret_cast<const u32x4 *>(xq + s * kI + g * 128 + sub * 16)));
     if (ok && sub == 0) term[f] = mul_rn(mul_rn((float)p, xs[s * G + g]), wsc[f]);
   });
-  if (t < kDnCols * G) wsc[RR * G + t] = ssv;
-  if (t < kI / 8) reinterpret_cast<u32x4 *>(xsh)[t] = hsh;
-  __syncthreads();
   Ls.consume([&](u32x4 w, int r, int g, int f, bool ok) {
     uint32_t wd[8];
     dequant16<BF16>(w, wsc[RR * G + f], wd);
@@ -531,20 +533,27 @@ __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
     if (ok && sub == 0) term[RR * G + f] = p;
   });
   __syncthreads();
-  if (t < kDnCols) {
-    float acc = 0.0f;
-    for (int s = 0; s < kTopK; ++s) {
-      const int r = s * kDnCols + t;
-      float v8 = 0.0f;
-      for (int g = 0; g < G; ++g) v8 = add_rn(v8, term[r * G + g]);
-      acc = round_bf16(acc + round_bf16(round_bf16(v8) * selw[s]));
-    }
+  // Epilogue in wave 0.  Lane r = s * kDnCols + c forms slot s's weighted
+  // term bf16(bf16(row sum) * w_s) of column c, which does not depend on the
+  // running sum; lanes 0 .. kDnCols - 1 then add the 8 terms in ascending
+  // slot order with a bf16 rounding after each add (int8.py:240-250), and the
+  // gated shared term.
+  if (t < RR) {
+    const int c = t & (kDnCols - 1);
+    float v8 = 0.0f;
+    for (int g = 0; g < G; ++g) v8 = add_rn(v8, term[t * G + g]);
+    prod[t] = round_bf16(round_bf16(v8) * selw[t / kDnCols]);
     float vs = 0.0f;
-    for (int g = 0; g < G; ++g) vs += term[(RR + t) * G + g];
-    const float vsh = round_bf16(vs);
-    const float sig = round_bf16(sigmoid_f32(glv));
-    const float out = round_bf16(acc + round_bf16(sig * vsh));
-    a.h[c0 + t] = f32_to_bf16_bits(bf16_bits_to_f32(hres) + out);
+    for (int g = 0; g < G; ++g) vs += term[(RR + c) * G + g];
+    const float shared = round_bf16(round_bf16(sigmoid_f32(glv)) * round_bf16(vs));
+    wave_lds_sync();
+    if (t < kDnCols) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int s = 0; s < kTopK; ++s) acc = round_bf16(acc + prod[s * kDnCols + t]);
+      const float out = round_bf16(acc + shared);
+      a.h[c0 + t] = f32_to_bf16_bits(bf16_bits_to_f32(hres) + out);
+    }
   }
 }
 
