@@ -226,77 +226,77 @@ __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
 }
 
 // Top-8 of the decode token over the 256 router logits (HF:770-774), with
-// all four waves of the workgroup: thread t holds expert t's logit v, and
-// every wave selects the 8 largest keys (logit desc, id asc) of its 64
-// experts; wave 0 then merges the four lists while wave 1 forms the softmax
-// denominator from v4, lane l's logits of experts 4 l .. 4 l + 3.  The
-// arithmetic (denominator order, fp32 softmax, renormalisation in rank
-// order, bf16 weights) is topk_wave's, so ids and weights equal the
-// single-wave selection bit for bit.  Fills sel/selw in combine order
-// (ascending expert id); workgroup (0, 0) publishes the routing for the down
-// kernel and the caller.  Every gate_up workgroup runs it on the same
-// inputs, so all of them agree.
+// all four waves of the workgroup: thread t holds expert t's logit v, every
+// wave selects the 8 largest keys (logit desc, id asc) of its 64 experts,
+// and after one barrier every wave merges the four lists itself, so no wave
+// waits on another again.  Lanes 0 .. 7 of the result hold the top 8 in
+// descending key order.  Every gate_up workgroup runs it on the same inputs,
+// so all of them agree.
 template <class KT>
-__device__ __forceinline__ void decode_select(const LayerArgs &a, float v, const float v4[4],
-                                              int *sel, float *selw) {
+__device__ __forceinline__ typename KT::T decode_top8(float v) {
   using T = typename KT::T;
   __shared__ T lists[4 * kTopK];
-  __shared__ float denom_s;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   T k = wave_top8(KT::make(v, t), lane);
   if (lane < kTopK) lists[wave * kTopK + lane] = k;
   __syncthreads();
-  if (wave == 0) {
-    k = lists[lane & 31];
-    k = merge_top8<15>(k, lane);
-    k = merge_top8<23>(k, lane);
-  } else if (wave == 1) {
-    T top = lists[0];
+  k = lists[lane & 31];
+  k = merge_top8<15>(k, lane);
+  return merge_top8<23>(k, lane);
+}
+
+// Expert id of combine slot `slot` (the slot-th smallest of the 8 selected
+// ids), from the merged keys k of decode_top8.
+template <class KT>
+__device__ __forceinline__ int decode_slot_expert(typename KT::T k, int slot) {
+  const int lane = threadIdx.x & 63;
+  const int id = clamp_index32(KT::index(k), kE);
+  int rank = 0;
 #pragma unroll
-    for (int w = 1; w < 4; ++w) {
-      const T o = lists[w * kTopK];
-      top = o > top ? o : top;
-    }
-    const float mx = KT::value(top);
-    float part = 0.0f;
+  for (int i = 0; i < kTopK; ++i)
+    rank += clamp_index32(KT::index(KT::readlane(k, i)), kE) < id ? 1 : 0;
+  const unsigned long long m = __ballot(lane < kTopK && rank == slot);
+  return __builtin_amdgcn_readlane(id, m ? (int)__builtin_ctzll(m) : 0);
+}
+
+// Routing weights of the selection and its publication for the down kernel
+// and the caller (one wave of workgroup 0): the softmax denominator from v4,
+// lane l's logits of experts 4 l .. 4 l + 3, fp32 softmax, renormalisation
+// in rank order, bf16 weights - topk_wave's arithmetic, so ids and weights
+// equal the single-wave selection bit for bit.  a.sel / a.selw are in combine
+// order (ascending expert id).
+template <class KT>
+__device__ __forceinline__ void decode_publish(const LayerArgs &a, typename KT::T k,
+                                               const float v4[4]) {
+  const int lane = threadIdx.x & 63;
+  const float mx = KT::value(KT::readlane(k, 0));
+  float part = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) part += expf(v4[j] - mx);
-    part = row_sum_f32(part);
-    const float d = (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 0)) +
-                     __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16))) +
-                    (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 32)) +
-                     __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 48)));
-    if (lane == 0) denom_s = d;
+  for (int j = 0; j < 4; ++j) part += expf(v4[j] - mx);
+  part = row_sum_f32(part);
+  const float d = (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 0)) +
+                   __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 16))) +
+                  (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 32)) +
+                   __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 48)));
+  const float pe = expf(KT::value(k) - mx) / d;
+  float psum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), 0));
+#pragma unroll
+  for (int i = 1; i < kTopK; ++i)
+    psum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), i));
+  const uint16_t wb = f32_to_bf16_bits(pe / psum);
+  const int id = clamp_index32(KT::index(k), kE);
+  int rank = 0;  // combine slot: rank of the id in ascending order (the ids are distinct)
+#pragma unroll
+  for (int i = 0; i < kTopK; ++i)
+    rank += clamp_index32(KT::index(KT::readlane(k, i)), kE) < id ? 1 : 0;
+  if (lane < kTopK) {
+    a.ids[lane] = id;
+    a.wts[lane] = wb;
+    if (a.ids_out) a.ids_out[lane] = id;
+    if (a.wts_out) a.wts_out[lane] = wb;
+    a.sel[rank] = id;
+    a.selw[rank] = bf16_bits_to_f32(wb);
   }
-  __syncthreads();
-  if (wave == 0) {
-    const float mx = KT::value(KT::readlane(k, 0));
-    const float pe = expf(KT::value(k) - mx) / denom_s;
-    float psum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), 0));
-#pragma unroll
-    for (int i = 1; i < kTopK; ++i)
-      psum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), i));
-    const uint16_t wb = f32_to_bf16_bits(pe / psum);
-    const int id = clamp_index32(KT::index(k), kE);
-    int rank = 0;  // combine slot: rank of the id in ascending order (the ids are distinct)
-#pragma unroll
-    for (int i = 0; i < kTopK; ++i)
-      rank += clamp_index32(KT::index(KT::readlane(k, i)), kE) < id ? 1 : 0;
-    if (lane < kTopK) {
-      const float w = bf16_bits_to_f32(wb);
-      sel[rank] = id;
-      selw[rank] = w;
-      if (blockIdx.x == 0) {
-        a.ids[lane] = id;
-        a.wts[lane] = wb;
-        if (a.ids_out) a.ids_out[lane] = id;
-        if (a.wts_out) a.wts_out[lane] = wb;
-        a.sel[rank] = id;
-        a.selw[rank] = w;
-      }
-    }
-  }
-  __syncthreads();
 }
 
 // Decode layer, second kernel: gate_up of one routed slot (W8A8),
@@ -320,8 +320,6 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
   __shared__ float term[R * G];
   __shared__ float wsh[2 * G];
   __shared__ float tsh[2 * G];
-  __shared__ int sel[kTopK];
-  __shared__ float selw[kTopK];
   const int t = threadIdx.x;
   // Workgroup b runs on XCD x = b % 8.  (slot, column) tiles are dealt out
   // so that the 8 workgroups writing one 128-byte line of a SwiGLU row (64
@@ -342,7 +340,7 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
   // all loads in flight where the branch joins.
   const float v = a.logits[t];
   const float4 f4 = *reinterpret_cast<const float4 *>(a.logits + (t & 63) * 4);
-  const float v4[4] = {f4.x, f4.y, f4.z, f4.w};  // used by wave 1
+  const float v4[4] = {f4.x, f4.y, f4.z, f4.w};  // for workgroup 0's routing weights
   const u32x4 xv = ldg16(a.xq + (t & (kH / 16 - 1)) * 16);
   const float xsv = a.xs[t & (G - 1)];
   const u32x4 xnv = ldg16(a.xn + t * (kH / 256));
@@ -351,11 +349,16 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
   Ls.issue(2, G, [&](int r) { return wq_sh + (int64_t)map_sh(r) * kH; });
   const int fs = t & (2 * G - 1);
   const float ssv = a.gu_s[(int64_t)kE * a.gu_ses + (int64_t)map_sh(fs / G) * G + fs % G];
-  if (a.router_bias)  // biased logits are fp32 values: 64-bit keys
-    decode_select<Key64>(a, v, v4, sel, selw);
-  else  // bf16 logits: 32-bit keys order them identically
-    decode_select<Key32>(a, v, v4, sel, selw);
-  const int e = clamp_index32(sel[slot], kE);
+  unsigned long long k64 = 0;
+  uint32_t k32 = 0;
+  int e;
+  if (a.router_bias) {  // biased logits are fp32 values: 64-bit keys
+    k64 = decode_top8<Key64>(v);
+    e = decode_slot_expert<Key64>(k64, slot);
+  } else {  // bf16 logits: 32-bit keys order them identically
+    k32 = decode_top8<Key32>(v);
+    e = decode_slot_expert<Key32>(k32, slot);
+  }
   const int8_t *wq = a.gu_q + (int64_t)e * a.gu_qes;
   const float my_scale = a.gu_s[(int64_t)e * a.gu_ses + (int64_t)map(t / G) * G + t % G];
   RowLoads<8> L;
@@ -406,6 +409,14 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
     }
     const float gate = round_bf16(sg), up = round_bf16(su);
     a.hbuf[slot * kI + n0 + t] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
+  }
+  // Workgroup 0 publishes the routing last: only the down kernel and the
+  // caller read it, so no workgroup's weight stream waits for the softmax.
+  if (b == 0 && t < 64) {
+    if (a.router_bias)
+      decode_publish<Key64>(a, k64, v4);
+    else
+      decode_publish<Key32>(a, k32, v4);
   }
 }
 
