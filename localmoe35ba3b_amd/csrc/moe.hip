@@ -105,12 +105,27 @@ struct LayerArgs {
 };
 
 // ------------------------------------------------------------------ decode
+// The norm weight of a layer that has none: zeros, so that the factor
+// (1 + w) is exactly 1 and both cases share one branch-free path.
+__device__ float g_zero_norm_w[kH];
+
+// Thread t's norm weights w[8 t .. 8 t + 7] as two 16-byte pieces, requested
+// unconditionally: a load under a branch would make the compiler wait for
+// every load in flight where the branch joins.
+struct NormW {
+  u32x4 lo, hi;
+};
+__device__ __forceinline__ NormW load_norm_w(const float *nw) {
+  const float *p = (nw ? nw : g_zero_norm_w) + threadIdx.x * (kH / 256);
+  return NormW{ldg16(p), ldg16(p + 4)};
+}
+
 // RMSNorm of one row of kH bf16 values (HF:807-815).  Thread t passes in
-// its chunk, values 8 t .. 8 t + 7, and receives them normalized and rounded
-// to bf16.  Fixed
-// reduction order (per-thread sum, 64-lane xor butterfly, the 4 wave sums
-// left to right, IEEE 1/sqrtf), which the oracle restates.
-__device__ __forceinline__ void norm_row(u32x4 raw, const float *nw, float eps, float *red,
+// its chunk, values 8 t .. 8 t + 7, and its norm weights, and receives the
+// chunk normalized and rounded to bf16.  Fixed reduction order (per-thread
+// sum, 64-lane xor butterfly, the 4 wave sums left to right, IEEE 1/sqrtf),
+// which the oracle restates.
+__device__ __forceinline__ void norm_row(u32x4 raw, const NormW &nw, float eps, float *red,
                                          float y[kH / 256]) {
   constexpr int PER = kH / 256;
   const int t = threadIdx.x;
@@ -130,15 +145,14 @@ __device__ __forceinline__ void norm_row(u32x4 raw, const float *nw, float eps, 
   const float r = 1.0f / sqrtf(tot / (float)kH + eps);
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    float yy = v[j] * r;
-    if (nw) yy = yy * (1.0f + nw[t * PER + j]);
-    y[j] = round_bf16(yy);
+    const float w = __uint_as_float(j < 4 ? nw.lo[j] : nw.hi[j - 4]);
+    y[j] = round_bf16((v[j] * r) * (1.0f + w));
   }
 }
 
 // The normalized row as LDS floats (bf16-rounded values); `raw` is thread
 // t's chunk of the row (values 8 t .. 8 t + 7).
-__device__ __forceinline__ void norm_row_to_lds(u32x4 raw, const float *nw, float eps, float *xf,
+__device__ __forceinline__ void norm_row_to_lds(u32x4 raw, const NormW &nw, float eps, float *xf,
                                                 float *red) {
   constexpr int PER = kH / 256;
   float y[PER];
@@ -171,10 +185,11 @@ __global__ __launch_bounds__(256) void decode_router_kernel(LayerArgs a) {
   const int e = ((b & 7) * (kRouterBlocks / 8) + (b >> 3)) * 4 + wave;
   const uint16_t *wrow = routed ? a.router_w + (int64_t)e * kH : a.gate_w;
   const u32x4 hrow = ldg16(a.h + t * (kH / 256));
+  const NormW nwv = load_norm_w(a.norm_w);
   u32x4 wv[kH / 512];
 #pragma unroll
   for (int j = 0; j < kH / 512; ++j) wv[j] = ldg16(wrow + lane * 8 + j * 512);
-  norm_row_to_lds(hrow, a.norm_w, a.eps, xf, red);
+  norm_row_to_lds(hrow, nwv, a.eps, xf, red);
 
   if (blockIdx.x < kH / 128) {
     const int g = blockIdx.x;
@@ -379,16 +394,6 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
                                                   *reinterpret_cast<const u32x4 *>(xp + 8)));
     if (ok && sub == 0) tsh[f] = p;
   });
-  __syncthreads();
-  if (t == 64) {
-    float sg = 0.0f, su = 0.0f;
-    for (int g = 0; g < G; ++g) {
-      sg = add_rn(sg, tsh[g]);
-      su = add_rn(su, tsh[G + g]);
-    }
-    const float gate = round_bf16(sg), up = round_bf16(su);
-    a.hbuf[kTopK * kI + nsh] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
-  }
   // The scales of the pairs a wave consumes are the ones its own threads
   // loaded (pair f = thread f), so they are handed over within the wave and
   // no workgroup barrier waits for them.
@@ -409,6 +414,14 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
     }
     const float gate = round_bf16(sg), up = round_bf16(su);
     a.hbuf[slot * kI + n0 + t] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
+  } else if (t == 64) {  // the shared column, from the terms of all four waves
+    float sg = 0.0f, su = 0.0f;
+    for (int g = 0; g < G; ++g) {
+      sg = add_rn(sg, tsh[g]);
+      su = add_rn(su, tsh[G + g]);
+    }
+    const float gate = round_bf16(sg), up = round_bf16(su);
+    a.hbuf[kTopK * kI + nsh] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
   }
   // Workgroup 0 publishes the routing last: only the down kernel and the
   // caller read it, so no workgroup's weight stream waits for the softmax.
@@ -586,6 +599,7 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a, int
   const u32x4 wv = tok < kE ? ldg16(a.router_w + (int64_t)tok * kH + t * PER)
                             : u32x4{0u, 0u, 0u, 0u};
   const u32x4 gv = ldg16(a.gate_w + t * PER);
+  const NormW nwv = load_norm_w(a.norm_w);
   auto router_row_norm = [&]() {
     float ss = 0.0f;
 #pragma unroll
@@ -603,7 +617,7 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a, int
     if (tok < kE) router_row_norm();
     return;
   }
-  norm_row_to_lds(ldg16(a.h + (int64_t)tok * kH + t * PER), a.norm_w, a.eps, xf, red);
+  norm_row_to_lds(ldg16(a.h + (int64_t)tok * kH + t * PER), nwv, a.eps, xf, red);
   {
     float ss = 0.0f;
 #pragma unroll
