@@ -124,6 +124,14 @@ __global__ __launch_bounds__(TH) void w8a8_gemv_kernel(GemvArgs a) {
   // so their wait does not include the weights: the two load latencies overlap.
   constexpr int QJ = 2 * MT * kGemvThreads / TH > 0 ? 2 * MT * kGemvThreads / TH : 1;
   constexpr int XN = MT * kGemvThreads / TH > 0 ? MT * kGemvThreads / TH : 1;
+  // Four or more rows at the model's K: the int8 products on the matrix
+  // cores (v_mfma_i32_16x16x64_i8).  The block's RB * G (row, group) pairs
+  // are 16 tasks of 16 rows x one 128-group, one per wave: two MFMAs give the
+  // group's exact int32 partials for 16 rows x 16 activation rows (rows past
+  // M are computed from a repeated row and dropped), where the VALU path
+  // would read every activation row from LDS once per weight piece.
+  constexpr bool MF = MT >= 4 && KC != 0 && TH == 1024;
+  static_assert(!MF || (32768 / KC) * (KC / 128) == 16 * (TH / 64), "one MFMA task per wave");
   const int th = threadIdx.x;
   if (rv.rvalid * G <= LD * 8 * (TH / 64) && M * G <= TH &&
       (QUANT ? M * G <= QJ * (TH / 32) : M * K <= XN * 16 * TH)) {
@@ -137,8 +145,20 @@ __global__ __launch_bounds__(TH) void w8a8_gemv_kernel(GemvArgs a) {
     const float xsv = (!QUANT && a.xs) ? ldg_f32(a.xs + (int64_t)(rv.xrow + ti / G) * G + ti % G) : 0.0f;
     const int tw = min(th, rv.rvalid * G - 1);
     const float wsv = PARTIALS ? 0.0f : ldg_f32(rv.s + (int64_t)rv.map(tw / G) * G + tw % G);
-    RowLoads<LD, TH> L;
-    L.issue(rv.rvalid, G, row_ptr);
+    RowLoads<MF ? 1 : LD, TH> L;
+    // MFMA task of this wave: rows 16 rb .. 16 rb + 15 of the block, group mg;
+    // lane l holds weight row 16 rb + (l & 15), bytes 16 (l >> 4) of each
+    // 64-K half of the group (the MFMA B layout).
+    const int lane = th & 63, rb = (th >> 6) / G, mg = (th >> 6) - rb * G;
+    const int mrow = 16 * rb + (lane & 15);
+    i32x4 mb[2];
+    if constexpr (MF) {
+      const int8_t *bp = row_ptr(min(mrow, rv.rvalid - 1)) + mg * 128 + (lane >> 4) * 16;
+      mb[0] = ldg<i32x4>(bp);
+      mb[1] = ldg<i32x4>(bp + 64);
+    } else {
+      L.issue(rv.rvalid, G, row_ptr);
+    }
     if constexpr (QUANT)
       qst.store(K, xq, xs);
     else
@@ -147,7 +167,25 @@ __global__ __launch_bounds__(TH) void w8a8_gemv_kernel(GemvArgs a) {
     if (!QUANT && a.xs) xs[ti] = xsv;
     if (!PARTIALS) ws[tw] = wsv;
     __syncthreads();
-    L.consume(body);
+    if constexpr (MF) {
+      // A: activation row (lane & 15) (repeated past MT), same bytes as B.
+      const int8_t *ap = xq + (lane & 15 & (MT - 1)) * K + mg * 128 + (lane >> 4) * 16;
+      i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(*reinterpret_cast<const i32x4 *>(ap), mb[0],
+                                                     i32x4{0, 0, 0, 0}, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_i32_16x16x64_i8(*reinterpret_cast<const i32x4 *>(ap + 64), mb[1], c,
+                                               0, 0, 0);
+      // C layout: lane l holds weight row 16 rb + (l & 15), activation rows
+      // 4 (l >> 4) .. 4 (l >> 4) + 3.
+      if (mrow < rv.rvalid) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 4 * (lane >> 4) + i;
+          if (m < M) part[m * RG + mrow * G + mg] = c[i];
+        }
+      }
+    } else {
+      L.consume(body);
+    }
     __syncthreads();
   } else {
     // Activations: quantize bf16 rows, or copy pre-quantized rows.

@@ -63,8 +63,8 @@ def test_act_quant_bit_exact(dev):
 
 
 # ------------------------------------------------------------- a5 W8A8
-@pytest.mark.parametrize('m', [1, 4, 8])
-@pytest.mark.parametrize('n,k', [(1024, 2048), (1000, 384), (2048, 512)])
+@pytest.mark.parametrize('m', [1, 4, 5, 8])
+@pytest.mark.parametrize('n,k', [(1024, 2048), (1000, 384), (2048, 512), (1000, 2048)])
 def test_w8a8_partials_bit_exact(dev, m, n, k):
     g = np.random.default_rng(m * 7 + n + k)
     xq = g.integers(-127, 128, size=(m, k)).astype(np.int8)
@@ -75,7 +75,7 @@ def test_w8a8_partials_bit_exact(dev, m, n, k):
     assert np.array_equal(p.cpu().numpy(), O.w8a8_partials(xq, wq))
 
 
-@pytest.mark.parametrize('m', [1, 4, 8])
+@pytest.mark.parametrize('m', [1, 4, 5, 8])
 def test_w8a8_linear_gate_up(dev, m):
     """The W8A8 decode linear: x bf16 [M, 2048], fused gate_up [1024, 2048]."""
     gen = seeded(2)
