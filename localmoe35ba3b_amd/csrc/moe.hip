@@ -319,9 +319,11 @@ __device__ __forceinline__ void decode_publish(const LayerArgs &a, typename KT::
 // K = kH, after the top-8.  The W8A8 per-group terms (f32(p) * xs_g) * ws_g
 // are formed by the lane that owns the partial and summed in ascending group
 // order by the epilogue (w8a8.py:40).  The grid is 512 workgroups, two per
-// CU; each also computes one column of the shared expert's gate_up + SwiGLU (W8A16 on the normalized row), whose inputs do
-// not depend on the routing: they are requested behind the logits and
-// consumed while the routed weights are in flight.
+// CU; each also computes one column of the shared expert's gate_up + SwiGLU
+// (W8A16 on the normalized row), whose inputs do not depend on the routing:
+// they are requested behind the logits and consumed while the routed
+// weights are in flight.  Workgroup 0 also publishes the routing (ids,
+// weights, combine order) after its own work.
 __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
   constexpr int G = kH / 128;
   constexpr int R = 2 * kGuPairs;
@@ -437,12 +439,13 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(LayerArgs a) {
 // shared expert for 8 output columns c0 .. c0 + 7 (W8A8 on the row-quantized
 // SwiGLU rows / W8A16), then the ascending-expert bf16 combine
 // (int8.py:240-250), the gated shared add and the residual add, in place.
-// The expert ids are requested first (scalar loads); everything that does
-// not depend on them - the shared expert's rows and scales, its SwiGLU row,
-// the residual columns, the gate logit - follows at once, and the routed
-// weights as soon as the ids land.  The 8 routed SwiGLU rows are quantized
-// per row (w8a8.quantize on [8, kI]) in one parallel pass: thread t owns
-// 16 values of row t / 32.
+// The expert ids are requested first (scalar loads); the small inputs that
+// do not depend on them - the routed and shared SwiGLU rows, the shared
+// expert's scales, the residual columns, the gate logit - follow at once,
+// then the routed scales and weights as soon as the ids land, and last the
+// shared expert's weight rows.  The 8 routed SwiGLU rows are quantized per
+// row (w8a8.quantize on [8, kI]) in one parallel pass: thread t owns 16
+// values of row t / 32.
 constexpr int kDnCols = 8;
 __global__ __launch_bounds__(256) void decode_down_kernel(LayerArgs a) {
   constexpr int G = kI / 128;
