@@ -60,6 +60,17 @@ const char *lm_last_error(void);
 int lm_quantize_weight_g128(const float *w, int8_t *q, float *s,
                             int64_t rows, int64_t k, void *stream);
 
+/* The 16-row tile layout of an int8 weight bank q [experts][n][k] (rows k
+ * bytes apart, experts expert_stride bytes apart), for the prefill GEMMs:
+ *   tiles[e * expert_stride + ((b * k/64 + s) * 1024) + 256 p + 16 r + j]
+ *     = q[e][16 b + r][64 s + 16 p + j],   r < 16, p < 4, j < 16.
+ * Each 16-row x 64-K block is 1 KB, its 16-byte pieces ordered piece-major,
+ * so lane 16 p + r of a wave loads exactly its MFMA operand piece.  tiles
+ * has q's size and expert stride; n % 16 == 0, k % 64 == 0.  No counterpart
+ * in the reference (a re-layout of convert.py's int8 format). */
+int lm_w8_tile_rows(const int8_t *q, int64_t experts, int64_t n, int64_t k,
+                    int64_t expert_stride, int8_t *tiles, void *stream);
+
 /* Dynamic activation quantization per row and 128-group:
  * s = max(amax, 1e-10) * (1/127), q = rint(x / s).  x [rows, k] (x_dtype).
  * Replaces w8a8.quantize / w8a8._quant (w8a8.py:8-22). */
@@ -263,6 +274,14 @@ typedef struct lm_moe_layer {
   int64_t gu_s_expert_stride;
   int64_t dn_q_expert_stride;
   int64_t dn_s_expert_stride;
+  /* Optional copies of gu_q and dn_q in the 16-row tile layout of
+   * lm_w8_tile_rows (same expert strides), which the prefill grouped GEMMs
+   * read with contiguous 1 KB wave loads; NULL = they read gu_q / dn_q.
+   * Results are identical either way.  No counterpart in the reference: a
+   * device-side cache of the bank (for callers that can spend the memory of
+   * a second int8 copy). */
+  const int8_t *gu_q_tiles;
+  const int8_t *dn_q_tiles;
 } lm_moe_layer;
 
 int64_t lm_moe_workspace_bytes(int64_t max_tokens, int64_t hidden,

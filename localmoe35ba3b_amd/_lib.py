@@ -28,6 +28,7 @@ SIGNATURES = {
     'lm_version': (ctypes.c_char_p, []),
     'lm_last_error': (ctypes.c_char_p, []),
     'lm_quantize_weight_g128': (I32, [P, P, P, I64, I64, P]),
+    'lm_w8_tile_rows': (I32, [P, I64, I64, I64, I64, P, P]),
     'lm_act_quant_g128': (I32, [P, I32, P, P, I64, I64, P]),
     'lm_w8a16_linear': (I32, [P, P, P, P, I64, I64, I64, I32, I32, P]),
     'lm_w8a16_grouped_gemv': (I32, [P, P, P, I64, I64, I64, I32, I32, I32, P]),
@@ -62,7 +63,8 @@ class MoeLayer(ctypes.Structure):
     _fields_ = [('router_w', P), ('router_bias', P), ('shared_gate_w', P), ('norm_w', P),
                 ('gu_q', P), ('gu_s', P), ('dn_q', P), ('dn_s', P),
                 ('gu_q_expert_stride', I64), ('gu_s_expert_stride', I64),
-                ('dn_q_expert_stride', I64), ('dn_s_expert_stride', I64)]
+                ('dn_q_expert_stride', I64), ('dn_s_expert_stride', I64),
+                ('gu_q_tiles', P), ('dn_q_tiles', P)]
 
 
 _lib = None

@@ -106,14 +106,16 @@ class Artifact:
         return gate_up, down
 
 
-def stack_from_artifact(root, device='cuda', layers=None, max_tokens=2048, verify=True):
+def stack_from_artifact(root, device='cuda', layers=None, max_tokens=2048, verify=True,
+                        prefill_tiles=True):
     """MoEStack of the fused layer path filled from a converted checkpoint.
 
     Per layer l: routed experts from mlp.experts.{gate_up_proj, down_proj};
     the shared expert (index E) from mlp.shared_expert.{gate_proj, up_proj}
     (rows concatenated) and .down_proj; router = mlp.gate.weight (bf16),
     shared gate = mlp.shared_expert_gate.weight, RMSNorm weight =
-    post_attention_layernorm.weight.
+    post_attention_layernorm.weight.  With prefill_tiles the prefill GEMMs
+    read a tile-layout copy of the int8 bank (MoEStack.build_prefill_tiles).
     """
     from .runtime.stack import MoEStack
     art = Artifact(root, verify=verify)
@@ -146,4 +148,6 @@ def stack_from_artifact(root, device='cuda', layers=None, max_tokens=2048, verif
                            .reshape(-1).to(torch.bfloat16))
         st.norm_w[l].copy_(art.load(p + '.post_attention_layernorm.weight', dev)['weight']
                            .reshape(-1).float())
+    if prefill_tiles:
+        st.build_prefill_tiles()
     return st

@@ -21,6 +21,8 @@
 //                        dequantized there.
 // In SwiGLU mode a tile's columns pair every gate column with its up partner
 // in the same lane.
+#include <type_traits>
+
 #include "internal.hpp"
 
 namespace lm {
@@ -42,6 +44,7 @@ struct GemmArgs {
   int64_t x_rows;
   const int8_t *q;
   int64_t q_es;
+  const int8_t *q_tiles;  // q in the 16-row tile layout (weight load mode kWlTiles)
   const float *s;
   int64_t s_es;
   uint16_t *y;
@@ -474,14 +477,20 @@ __device__ __forceinline__ void barrier_raw() { asm volatile("s_barrier" ::: "me
 // lane and step reads the same k from LDS, so each product pairs the right x
 // and w (a fixed permutation of the summation order inside the stage).
 //
-// Streamed weights (RP = true: the routed GEMMs, which read each expert's
-// weights once) are not loaded in that layout: there a quarter-wave touches
-// 16 rows 2 KB apart, which keeps the address path busy with 16 cache lines
-// per quarter-wave.  Instead quarter-wave a loads 64 contiguous bytes of each
-// of rows 4 a .. 4 a + 3 (lane 16 a + 4 b + p: row 4 a + b, piece p), 4 lines
-// per quarter-wave, and one ds_bpermute per dword moves piece p of row r to
-// lane 16 p + r while the previous stage's MFMAs run.  Dense weights, which
-// every row tile re-reads from cache, are loaded in the MFMA layout directly.
+// Weight load modes (WL):
+//   kWlDirect  dense weights, which every row tile re-reads from cache: each
+//              lane loads its MFMA operand piece directly (a quarter-wave
+//              touches 16 rows 2 KB apart);
+//   kWlPermute streamed (routed) weights in the standard layout: quarter-wave
+//              a loads 64 contiguous bytes of each of rows 4 a .. 4 a + 3
+//              (lane 16 a + 4 b + p: row 4 a + b, piece p), 4 lines per
+//              quarter-wave instead of 16, and one ds_bpermute per dword
+//              moves piece p of row r to lane 16 p + r while the previous
+//              stage's MFMAs run;
+//   kWlTiles   streamed weights in the 16-row tile layout (lm_w8_tile_rows):
+//              a wave's load of one 16-row x 64-K block is 1 KB contiguous
+//              and lands in the MFMA layout, no permute.
+constexpr int kWlDirect = 0, kWlPermute = 1, kWlTiles = 2;
 //
 // A stage in LDS: BM rows x 128 B (64 bf16); 16-byte chunk p of row r is
 // stored at chunk p ^ rb_swz(r).  Scales of the tile are staged once,
@@ -502,7 +511,7 @@ __device__ __forceinline__ int rb_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); 
 // consecutive lanes read 64 contiguous bytes of a weight row.  Weights are
 // requested BD - 1 stages ahead, activation rows AD stages ahead (AD - 1
 // stages wait in registers, one more in LDS).
-template <typename T, bool SWIGLU, bool GATHER, bool RP, int K, int BM, int TN, int BD, int HL, int AD,
+template <typename T, bool SWIGLU, bool GATHER, int WL, int K, int BM, int TN, int BD, int HL, int AD,
           int NW, int MS>
 __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t start, int rows,
                                         int nt, unsigned char *smem) {
@@ -562,15 +571,23 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
     const int wr = wrow(piece / (G / 4));
     sreg[j] = ldg16(wsc + (int64_t)(wr >= 0 ? wr : 0) * G + (piece % (G / 4)) * 4);
   }
-  // Weight sources, bytes (+ 64 h) of each stage: with RP, lane 16 a + 4 b + p
-  // loads column col_base(ni) + 4 a + b, bytes 16 p, and rb_perm moves them into
-  // the MFMA layout; otherwise lane l loads column col_base(ni) + (l & 15),
-  // bytes 16 q.
+  // Weight sources of column sub-tile ni (16 weight rows from a multiple of
+  // 16), stage 0.  kWlDirect: lane l loads column col_base(ni) + (l & 15),
+  // bytes 16 q (+ 64 h).  kWlPermute: lane 16 a + 4 b + p loads column
+  // col_base(ni) + 4 a + b, bytes 16 p, and rb_perm moves them into the MFMA
+  // layout.  kWlTiles: the sub-tile's 1 KB tile of each 64-K block, byte 16 l.
   const int8_t *bsrc[NI];
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    const int wr = wrow(col_base(ni) + (RP ? 4 * q + ((lane & 15) >> 2) : lane & 15));
-    bsrc[ni] = wq + (int64_t)(wr >= 0 ? wr : 0) * K + (RP ? lane & 3 : q) * 16;
+    if constexpr (WL == kWlTiles) {
+      const int wr = wrow(col_base(ni));
+      bsrc[ni] = a.q_tiles + e * a.q_es + (int64_t)((wr >= 0 ? wr : 0) >> 4) * (K / 64) * 1024 +
+                 lane * 16;
+    } else {
+      const int wr =
+          wrow(col_base(ni) + (WL == kWlPermute ? 4 * q + ((lane & 15) >> 2) : lane & 15));
+      bsrc[ni] = wq + (int64_t)(wr >= 0 ? wr : 0) * K + (WL == kWlPermute ? lane & 3 : q) * 16;
+    }
   }
   // Activation sources: wave-load j fills rows RPL (4 j + wave) ..; lane ->
   // row RPL (4 j + wave) + lane / CPR, LDS chunk lane % CPR, which holds the
@@ -590,7 +607,7 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   // (a byte address for ds_bpermute).
   const int perm_src = 4 * (16 * ((lane & 15) >> 2) + 4 * (lane & 3) + q);
   auto rb_perm = [&](int slot) {
-    if constexpr (RP) {
+    if constexpr (WL == kWlPermute) {
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
@@ -605,7 +622,9 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
-      for (int h = 0; h < HL; ++h) breg[slot][ni][h] = ldg16(bsrc[ni] + s * KS + 64 * h);
+      for (int h = 0; h < HL; ++h)
+        breg[slot][ni][h] = ldg16(bsrc[ni] + (WL == kWlTiles ? (s * HL + h) * 1024
+                                                             : s * KS + 64 * h));
   };
   auto load_a = [&](int slot, int s) {
 #pragma unroll
@@ -758,7 +777,7 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   }
 }
 
-template <typename T, bool SWIGLU, bool GATHER, bool RP, int K, int BM, int TN, int BD, int HL,
+template <typename T, bool SWIGLU, bool GATHER, int WL, int K, int BM, int TN, int BD, int HL,
           int AD, int NW, int OCC>
 __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
   constexpr int SC_BYTES = NW * TN * (K / 128) * 4;
@@ -780,13 +799,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
   if (rows <= 0) return;
   static_assert(BM == 96, "row-count dispatch below covers 96-row tiles");
   if (rows > 80)
-    rb_tile<T, SWIGLU, GATHER, RP, K, BM, TN, BD, HL, AD, NW, 6>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 6>(a, e, start, rows, nt, smem);
   else if (rows > 64)
-    rb_tile<T, SWIGLU, GATHER, RP, K, BM, TN, BD, HL, AD, NW, 5>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 5>(a, e, start, rows, nt, smem);
   else if (rows > 32)
-    rb_tile<T, SWIGLU, GATHER, RP, K, BM, TN, BD, HL, AD, NW, 4>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 4>(a, e, start, rows, nt, smem);
   else
-    rb_tile<T, SWIGLU, GATHER, RP, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem);
 }
 
 // Configuration of grouped_rb_kernel, chosen by measurement on the
@@ -801,9 +820,9 @@ constexpr int kRbAD = 2;
 constexpr int kRbNW = 4;
 constexpr int kGroupedBN = 128;  // grouped_mfma_kernel tile columns
 
-// RP: reassigned weight loads + permute (weights streamed once, the routed
-// GEMMs); dense weights are loaded in the MFMA layout directly.
-template <typename T, bool SWIGLU, bool GATHER, bool RP>
+// WL: weight load mode (kWlDirect for dense weights, kWlPermute or kWlTiles
+// for the routed GEMMs, which stream each expert's weights once).
+template <typename T, bool SWIGLU, bool GATHER, int WL>
 static int launch_grouped(GemmArgs a, unsigned mtiles, hipStream_t st) {
   if (mtiles == 0) return LM_OK;
   if (a.tile_rows <= 96 && (a.K == 2048 || a.K == 512)) {
@@ -813,10 +832,10 @@ static int launch_grouped(GemmArgs a, unsigned mtiles, hipStream_t st) {
     const int64_t grid = xcd_grid(a.mt_count, a.nt_count);
     LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
     if (a.K == 2048)
-      grouped_rb_kernel<T, SWIGLU, GATHER, RP, 2048, 96, kRbTN, kRbBD, kRbHL, kRbAD, kRbNW, kRbOcc>
+      grouped_rb_kernel<T, SWIGLU, GATHER, WL, 2048, 96, kRbTN, kRbBD, kRbHL, kRbAD, kRbNW, kRbOcc>
           <<<(unsigned)grid, kRbNW * 64, 0, st>>>(a);
     else
-      grouped_rb_kernel<T, SWIGLU, GATHER, RP, 512, 96, kRbTN, kRbBD, kRbHL, kRbAD, kRbNW, kRbOcc>
+      grouped_rb_kernel<T, SWIGLU, GATHER, WL, 512, 96, kRbTN, kRbBD, kRbHL, kRbAD, kRbNW, kRbOcc>
           <<<(unsigned)grid, kRbNW * 64, 0, st>>>(a);
     return check_launch("grouped_rb_kernel");
   }
@@ -859,8 +878,8 @@ int w8a16_gemm_dense(const void *x, const int8_t *q, const float *s, void *y, in
   // because each wave dequantizes only its own columns' weights.
   if (k == 2048 || k == 512) {
     a.tile_rows = 96;
-    return dtype == LM_BF16 ? launch_grouped<BF16, false, false, false>(a, cdiv(m, 96), st)
-                            : launch_grouped<FP16, false, false, false>(a, cdiv(m, 96), st);
+    return dtype == LM_BF16 ? launch_grouped<BF16, false, false, kWlDirect>(a, cdiv(m, 96), st)
+                            : launch_grouped<FP16, false, false, kWlDirect>(a, cdiv(m, 96), st);
   }
   const unsigned mt = cdiv(m, 128);
   if (dtype == LM_BF16) return launch_gemm<BF16, 128, 2, false, false, true>(a, mt, st);
@@ -870,11 +889,19 @@ int w8a16_gemm_dense(const void *x, const int8_t *q, const float *s, void *y, in
 template <typename T>
 static int routed_dispatch(const GemmArgs &a, unsigned mt, bool gather, bool swiglu,
                            hipStream_t st) {
-  if (swiglu)
-    return gather ? launch_grouped<T, true, true, true>(a, mt, st)
-                  : launch_grouped<T, true, false, true>(a, mt, st);
-  return gather ? launch_grouped<T, false, true, true>(a, mt, st)
-                : launch_grouped<T, false, false, true>(a, mt, st);
+  // The tile layout serves the fused layer's two GEMMs (gathered gate_up +
+  // SwiGLU, contiguous down) in bf16; every other form reads q.
+  const bool tiles = a.q_tiles != nullptr && std::is_same<T, BF16>::value;
+  if (swiglu) {
+    if (gather)
+      return tiles ? launch_grouped<T, true, true, kWlTiles>(a, mt, st)
+                   : launch_grouped<T, true, true, kWlPermute>(a, mt, st);
+    return launch_grouped<T, true, false, kWlPermute>(a, mt, st);
+  }
+  if (!gather)
+    return tiles ? launch_grouped<T, false, false, kWlTiles>(a, mt, st)
+                 : launch_grouped<T, false, false, kWlPermute>(a, mt, st);
+  return launch_grouped<T, false, true, kWlPermute>(a, mt, st);
 }
 
 int routed_gemm(const RoutedGemm &r, hipStream_t st) {
@@ -888,10 +915,13 @@ int routed_gemm(const RoutedGemm &r, hipStream_t st) {
   a.x_rows = r.x_rows;
   a.q = r.q;
   a.q_es = r.q_es;
+  a.q_tiles = r.q_tiles;
   a.s = r.s;
   a.s_es = r.s_es;
   a.y = static_cast<uint16_t *>(r.y);
   a.ldy = r.swiglu ? r.n / 2 : r.n;
+  LM_REQUIRE(!r.q_tiles || (r.n % 32 == 0 && r.k % 64 == 0), LM_EINVAL,
+             "the tile layout needs n % 32 == 0 and k % 64 == 0");
   a.N = (int)r.n;
   a.K = (int)r.k;
   a.tile_rows = (int)r.bm;

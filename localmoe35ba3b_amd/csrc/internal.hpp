@@ -30,6 +30,7 @@ struct RoutedGemm {
   int64_t y_rows, n, k;
   bool gather, swiglu;
   int dtype;
+  const int8_t *q_tiles = nullptr;  // q in the lm_w8_tile_rows layout, or null
 };
 int routed_gemm(const RoutedGemm &r, hipStream_t st);
 

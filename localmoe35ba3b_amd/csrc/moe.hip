@@ -1302,12 +1302,15 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   if (int rc = mark(4)) return rc;
   // gate_up over the T token rows gathered through pos, down over the R + T
   // rows of hbuf; the banks hold E + 1 experts (index E = shared expert)
-  const RoutedGemm gu{a.xn, kH, T, a.gu_q, a.gu_s, a.gu_qes, a.gu_ses, kE + 1, pos, table,
-                      w.n_tiles, kBM, a.hbuf, R + T, 2 * kI, kH, true, true, LM_BF16};
+  // (the weights' tile-layout copies, when the caller provides them)
+  const RoutedGemm gu{a.xn,    kH,      T,  a.gu_q, a.gu_s,  a.gu_qes, a.gu_ses,
+                      kE + 1,  pos,     table, w.n_tiles, kBM, a.hbuf, R + T,
+                      2 * kI,  kH,      true,  true,   LM_BF16, layer->gu_q_tiles};
   if (int rc = routed_gemm(gu, st)) return rc;
   if (int rc = mark(5)) return rc;
-  const RoutedGemm dn{a.hbuf, kI, R + T, a.dn_q, a.dn_s, a.dn_qes, a.dn_ses, kE + 1, pos, table,
-                      w.n_tiles, kBM, vbuf, R + T, kH, kI, false, false, LM_BF16};
+  const RoutedGemm dn{a.hbuf,  kI,      R + T, a.dn_q, a.dn_s, a.dn_qes, a.dn_ses,
+                      kE + 1,  pos,     table, w.n_tiles, kBM, vbuf, R + T,
+                      kH,      kI,      false, false,  LM_BF16, layer->dn_q_tiles};
   if (int rc = routed_gemm(dn, st)) return rc;
   if (int rc = mark(6)) return rc;
   prefill_combine_kernel<<<(unsigned)T, 256, 0, st>>>(a, rpos, vbuf, R);

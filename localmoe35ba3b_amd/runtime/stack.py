@@ -87,6 +87,7 @@ class MoEStack:
         _lib.call('lm_moe_workspace_init', self.workspace.data_ptr(), nbytes, _lib.stream(dev))
         self._structs = [self._layer_struct(l) for l in range(layers)]
         self._side = self._side_ws = None  # second stream and workspace of prefill_
+        self.gu_q_tiles = self.dn_q_tiles = None  # see build_prefill_tiles
 
     # ------------------------------------------------------------------ views
     def bank_bytes(self):
@@ -94,6 +95,24 @@ class MoEStack:
         if self.norm_w is not None:
             tensors.append(self.norm_w)
         return sum(t.numel() * t.element_size() for t in tensors)
+
+    def build_prefill_tiles(self):
+        """Copies of gu_q and dn_q in the 16-row tile layout (lm_w8_tile_rows)
+        for the prefill grouped GEMMs, which then read each 16-row x 64-K
+        weight block as one contiguous 1 KB wave load.  Costs a second int8
+        bank in HBM (about 32 GB for 40 layers); results are identical with
+        or without.  Call again after changing gu_q / dn_q."""
+        if self.gu_q_tiles is None:
+            self.gu_q_tiles = torch.empty_like(self.gu_q)
+            self.dn_q_tiles = torch.empty_like(self.dn_q)
+        st = _lib.stream(self.device)
+        for l in range(self.L):
+            for q, t in ((self.gu_q, self.gu_q_tiles), (self.dn_q, self.dn_q_tiles)):
+                _lib.call('lm_w8_tile_rows', q[l].data_ptr(), q.shape[1], q.shape[2], q.shape[3],
+                          q.stride(1), t[l].data_ptr(), st)
+            self._structs[l].gu_q_tiles = self.gu_q_tiles[l].data_ptr()
+            self._structs[l].dn_q_tiles = self.dn_q_tiles[l].data_ptr()
+        return self
 
     def _layer_struct(self, l):
         s = _lib.MoeLayer()
@@ -258,10 +277,12 @@ class MoEStack:
 class SyntheticMoEStack(MoEStack):
     """Random-init 35B-A3B-class MoE-FFN stack resident in HBM: weights drawn
     on the GPU from per-(layer, matrix) seeds, N(0, 0.02) fp32, quantized by
-    the group-128 HIP quantizer; RMSNorm weight zero."""
+    the group-128 HIP quantizer; RMSNorm weight zero.  With prefill_tiles the
+    prefill GEMMs read a tile-layout copy of the int8 bank
+    (build_prefill_tiles)."""
 
     def __init__(self, layers=40, seed=4, device='cuda', max_tokens=2048, router_bias=None,
-                 chunk_experts=32):
+                 chunk_experts=32, prefill_tiles=True):
         super().__init__(layers, device, max_tokens, router_bias)
         dev = self.device
         E1 = self.E + 1
@@ -282,3 +303,5 @@ class SyntheticMoEStack(MoEStack):
                 w = torch.randn((c1 - c0, self.H, self.I), generator=gen, device=dev) * 0.02
                 self.dn_q[l, c0:c1], self.dn_s[l, c0:c1] = quantize_g128(w)
                 del w
+        if prefill_tiles:
+            self.build_prefill_tiles()

@@ -308,3 +308,34 @@ def test_prefill_weights_vs_exact_router(dev, capsys):
         print(f'\n[prefill router] weights differing from the all-exact router: '
               f'{mismatched} of {total} ({rate:.2e})')
     assert rate < 1e-2
+
+
+def test_tile_rows_layout(dev):
+    """lm_w8_tile_rows against the index formula of its declaration, on a
+    bank whose experts sit further apart than n * k (the stride is kept)."""
+    from localmoe35ba3b_amd import _lib
+    g = np.random.default_rng(7)
+    E, n, k, es = 3, 48, 192, 48 * 192 + 1024
+    flat = g.integers(-127, 128, size=E * es).astype(np.int8)
+    q = torch.from_numpy(flat).to(dev)
+    tiles = torch.zeros_like(q)
+    _lib.call('lm_w8_tile_rows', q.data_ptr(), E, n, k, es, tiles.data_ptr(), _lib.stream(dev))
+    got = tiles.cpu().numpy()
+    ref = np.zeros_like(flat)
+    for e in range(E):
+        w = flat[e * es:e * es + n * k].reshape(n // 16, 16, k // 64, 4, 16)  # b, r, s, p, j
+        ref[e * es:e * es + n * k] = w.transpose(0, 2, 3, 1, 4).reshape(-1)  # b, s, p, r, j
+    assert np.array_equal(got, ref)
+
+
+def test_prefill_tiles_bit_identical(dev):
+    """The prefill GEMMs reading the tile-layout copy of the bank give the
+    same layer output and routing as reading the bank itself."""
+    st = SyntheticMoEStack(layers=1, seed=71, device=dev, max_tokens=2048, prefill_tiles=False)
+    h = inputs(2048, 71, dev)
+    plain, ids0, w0 = run_layer(st, h)
+    st.build_prefill_tiles()
+    tiled, ids1, w1 = run_layer(st, h)
+    assert torch.equal(ids0, ids1) and torch.equal(w0, w1)
+    assert torch.equal(plain, tiled)
+    del st
