@@ -950,9 +950,9 @@ __global__ __launch_bounds__(kTopkTokens * 64) void prefill_topk_count_kernel(La
 // offs[e] + (routes to e of earlier top-k workgroups) + rank inside its own
 // workgroup.  Each workgroup handles kScanRoutes routes and sums the bcounts
 // columns itself (nb rows of kE byte counts, 64 KB for 2048 tokens), so no
-// grid-wide step is needed.  Workgroup 0 also writes the tile table (kBM-row
-// tiles per expert, surplus rows (0, 0, 0), then the shared expert's tiles
-// over rows [R, R + T)) and the shared rows' tokens.
+// grid-wide step is needed.  Workgroup 0 also writes the tile table (the
+// shared expert's tiles over rows [R, R + T), then kBM-row tiles per routed
+// expert, then surplus rows (0, 0, 0)) and the shared rows' tokens.
 //
 // Every load of a phase is issued unconditionally (clamped rows), so the
 // phase pays one load latency, not one per row.
@@ -1037,27 +1037,29 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
     rpos[r] = p;
   }
   if (blockIdx.x != 0) return;
-  // Tile table: thread e writes the tiles of expert e at its exclusive tile
-  // prefix; rows past the last tile up to max_tiles are (0, 0, 0).
+  // Tile table: the shared expert's nst full tiles over rows [R, R + T)
+  // first (the longest tiles start first), then thread e writes the tiles of
+  // routed expert e at nst + its exclusive tile prefix, and rows past the
+  // last tile up to nst + max_tiles are (0, 0, 0).
+  const int nst = (T + kBM - 1) / kBM;
   const int nt = t < kE ? (c + kBM - 1) / kBM : 0;
   int ntot = 0;
   const int tex = scan(nt, &ntot);
   for (int k = 0; k < nt; ++k) {
-    const int64_t i = tex + k;
+    const int64_t i = nst + tex + k;
     table[i * 3] = t;
     table[i * 3 + 1] = offs[t] + (int64_t)k * kBM;
     table[i * 3 + 2] = offs[t + 1];
   }
-  for (int i = ntot + t; i < max_tiles; i += 1024) {
+  for (int i = nst + ntot + t; i < nst + max_tiles; i += 1024) {
     table[(int64_t)i * 3] = 0;
     table[(int64_t)i * 3 + 1] = 0;
     table[(int64_t)i * 3 + 2] = 0;
   }
-  const int nst = (T + kBM - 1) / kBM;
   for (int j = t; j < nst; j += 1024) {
-    table[(int64_t)(max_tiles + j) * 3] = kE;
-    table[(int64_t)(max_tiles + j) * 3 + 1] = R + (int64_t)j * kBM;
-    table[(int64_t)(max_tiles + j) * 3 + 2] = R + T;
+    table[(int64_t)j * 3] = kE;
+    table[(int64_t)j * 3 + 1] = R + (int64_t)j * kBM;
+    table[(int64_t)j * 3 + 2] = R + T;
   }
   for (int tok = t; tok < T; tok += 1024) pos[R + tok] = tok;
 }
