@@ -5,7 +5,8 @@ One step = one request of the headline workload: a 4096-token prefill in two
 behind the first on a second stream, both 40-layer passes replayed as one HIP
 graph) followed by 33 serial decode tokens (W8A8 expert
 GEMVs, the 40-layer decode step replayed as a HIP graph), over random-init
-int8 group-128 weights (~33.4 GB) resident in HBM.
+int8 group-128 weights (~33.4 GB) resident in HBM, plus the 16-row tile-layout
+copy of the int8 bank (~32.4 GB) that the prefill grouped GEMMs read.
 
 Prints one JSON line.  value = prefill tok/s; decode tok/s, decode HBM GB/s
 and the roofline of the dominant kernel ride along.  Per-kernel times come
@@ -557,6 +558,7 @@ def main():
             kernels[p] = {'avg_us': round(avg_us, 2), 'launches': n_dec,
                           'bytes_per_launch': dec_bytes[p],
                           'gbs': round(dec_bytes[p] / avg_us / 1e3, 1),
+                          'hbm_frac': round(dec_bytes[p] / avg_us / 1e3 / HBM_PEAK_GBS, 4),
                           'ms_per_request': round(avg_us * L * DECODE_TOKENS / 1e3, 3)}
 
     # dominant kernel by total time within one request
@@ -616,7 +618,8 @@ def main():
                    'layers': L, 'prefill_tokens': PREFILL_TOKENS, 'chunk': CHUNK,
                    'prefill_schedule': 'chunk 2 enters layer l once chunk 1 has left layer '
                                        'l-1 (second stream); one HIP graph',
-                   'decode_tokens': DECODE_TOKENS, 'bank_gb': round(stack.bank_bytes() / 1e9, 2)},
+                   'decode_tokens': DECODE_TOKENS, 'bank_gb': round(stack.bank_bytes() / 1e9, 2),
+                   'prefill_tile_copy_gb': round(stack.tile_bytes() / 1e9, 2)},
         'prefill_tok_s': round(prefill_tok_s, 1),
         'prefill_ms_steps': [round(t, 3) for t in pf_steps],
         'decode_ms_steps': [round(t, 3) for t in dec_steps],

@@ -96,6 +96,12 @@ class MoEStack:
             tensors.append(self.norm_w)
         return sum(t.numel() * t.element_size() for t in tensors)
 
+    def tile_bytes(self):
+        """Bytes of the prefill tile copy (0 when build_prefill_tiles has not run)."""
+        if self.gu_q_tiles is None:
+            return 0
+        return (self.gu_q_tiles.numel() + self.dn_q_tiles.numel()) * self.gu_q_tiles.element_size()
+
     def build_prefill_tiles(self):
         """Copies of gu_q and dn_q in the 16-row tile layout (lm_w8_tile_rows)
         for the prefill grouped GEMMs, which then read each 16-row x 64-K
