@@ -479,9 +479,26 @@ def main():
         for l in range(L):
             stack.layer_forward(static, l, events=dec_ev[l])
 
-    for _ in range(args.warmup):
+    def step(m=None):
+        """One step: the timed prefill and decode, then the per-kernel probes."""
+        if m is not None:
+            m[0].record()
         prefill()
+        if m is not None:
+            m[1].record()
         decode()
+        if m is not None:
+            m[2].record()
+        if dec_ev is not None:
+            decode_kernel_probe()
+        if pf_events is not None:
+            prefill_kernel_probe()
+            torch.cuda.synchronize()
+
+    # Warm-up steps do a timed step's work, probes included, so the first
+    # timed step starts from the state every later one starts from.
+    for _ in range(args.warmup):
+        step()
     torch.cuda.synchronize()
     log('warmup done')
 
@@ -491,17 +508,8 @@ def main():
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     for s in range(args.steps):
-        m = marks[s]
-        m[0].record()
-        prefill()
-        m[1].record()
-        decode()
-        m[2].record()
-        if dec_ev is not None:
-            decode_kernel_probe()
+        step(marks[s])
         if pf_events is not None:
-            prefill_kernel_probe()
-            torch.cuda.synchronize()
             for l in range(L):
                 ev = pf_events[l]
                 for i, p in enumerate(PREFILL_PHASES):

@@ -809,36 +809,47 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
 }
 
 // Configuration of grouped_rb_kernel, chosen by measurement on the
-// 2048-token prefill chunk: 4 waves of 32 columns each, a 3-slot weight ring
-// of one 64-K piece per stage, activations prefetched 2 stages ahead, a
-// register budget for 3 workgroups per CU.
+// 2048-token prefill chunk: 4 waves of TN columns each, a 3-slot weight ring
+// of one 64-K piece per stage, activations prefetched 2 stages ahead and a
+// register budget for OCC workgroups per CU.  The routed GEMMs on the tile
+// layout (kWlTiles) use 64 columns per wave at 2 workgroups per CU: a tile
+// streams 512 KB of one expert's weights and its activation rows are re-read
+// half as often as with 32 columns.  On the 40-layer stack, two chunks
+// overlapped, that is 3 % more prefill tokens/s, though each GEMM alone is
+// 1-2 % slower (and 8 % on a Zipf-skewed chunk, whose hot expert is compute
+// bound at the lower occupancy).  Every other use keeps 32 columns at 3 per CU.
 constexpr int kRbTN = 32;
+constexpr int kRbOcc = 3;
+constexpr int kRbTnTiles = 64;
+constexpr int kRbOccTiles = 2;
 constexpr int kRbBD = 3;
 constexpr int kRbHL = 1;
-constexpr int kRbOcc = 3;
 constexpr int kRbAD = 2;
 constexpr int kRbNW = 4;
 constexpr int kGroupedBN = 128;  // grouped_mfma_kernel tile columns
+
+template <typename T, bool SWIGLU, bool GATHER, int WL, int K>
+static int launch_rb(GemmArgs a, unsigned mtiles, hipStream_t st) {
+  constexpr int TN = WL == kWlTiles ? kRbTnTiles : kRbTN;
+  constexpr int OCC = WL == kWlTiles ? kRbOccTiles : kRbOcc;
+  constexpr int RBN = kRbNW * TN;
+  a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, RBN / 2) : (int)cdiv(a.N, RBN);
+  a.mt_count = (int)mtiles;
+  const int64_t grid = xcd_grid(a.mt_count, a.nt_count);
+  LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
+  grouped_rb_kernel<T, SWIGLU, GATHER, WL, K, 96, TN, kRbBD, kRbHL, kRbAD, kRbNW, OCC>
+      <<<(unsigned)grid, kRbNW * 64, 0, st>>>(a);
+  return check_launch("grouped_rb_kernel");
+}
 
 // WL: weight load mode (kWlDirect for dense weights, kWlPermute or kWlTiles
 // for the routed GEMMs, which stream each expert's weights once).
 template <typename T, bool SWIGLU, bool GATHER, int WL>
 static int launch_grouped(GemmArgs a, unsigned mtiles, hipStream_t st) {
   if (mtiles == 0) return LM_OK;
-  if (a.tile_rows <= 96 && (a.K == 2048 || a.K == 512)) {
-    constexpr int RBN = kRbNW * kRbTN;
-    a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, RBN / 2) : (int)cdiv(a.N, RBN);
-    a.mt_count = (int)mtiles;
-    const int64_t grid = xcd_grid(a.mt_count, a.nt_count);
-    LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
-    if (a.K == 2048)
-      grouped_rb_kernel<T, SWIGLU, GATHER, WL, 2048, 96, kRbTN, kRbBD, kRbHL, kRbAD, kRbNW, kRbOcc>
-          <<<(unsigned)grid, kRbNW * 64, 0, st>>>(a);
-    else
-      grouped_rb_kernel<T, SWIGLU, GATHER, WL, 512, 96, kRbTN, kRbBD, kRbHL, kRbAD, kRbNW, kRbOcc>
-          <<<(unsigned)grid, kRbNW * 64, 0, st>>>(a);
-    return check_launch("grouped_rb_kernel");
-  }
+  if (a.tile_rows <= 96 && (a.K == 2048 || a.K == 512))
+    return a.K == 2048 ? launch_rb<T, SWIGLU, GATHER, WL, 2048>(a, mtiles, st)
+                       : launch_rb<T, SWIGLU, GATHER, WL, 512>(a, mtiles, st);
   constexpr int BN = kGroupedBN;
   a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, BN / 2) : (int)cdiv(a.N, BN);
   a.mt_count = (int)mtiles;
