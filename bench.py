@@ -180,7 +180,10 @@ def isolated_probe(dev, spin_cycles, reps=32):
     HBM.  Covers the dense W8A16 linear [4096, 2048] at 1 and 2048 rows, the
     W8A8 gate_up + SwiGLU [1024, 2048] at 1, 4 and 8 rows, and the int8 MFMA
     W8A8 GEMM at 2048 x 4096 x 2048 (the one-token MoE layer is the stack's
-    decode layer, timed per kernel in the request)."""
+    decode layer, timed per kernel in the request).  The GEMVs also report
+    `graph_us`, the per-launch time of 64 launches replayed as one HIP graph,
+    and `launch_floor` gives both timings of a one-element fill: per-launch
+    events cost about as much as a short kernel itself."""
     from localmoe35ba3b_amd.convert import quantize_g128
     from localmoe35ba3b_amd.operators import int8, w8a8
     gen = torch.Generator(device=dev)
@@ -198,12 +201,44 @@ def isolated_probe(dev, spin_cycles, reps=32):
         torch.cuda.synchronize()
         return sorted(ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(n))[n // 2]
 
-    def hbm(us, nbytes, shape):
-        return {'avg_us': round(us, 2), 'bytes_per_launch': nbytes,
-                'gbs': round(nbytes / us / 1e3, 1),
-                'hbm_frac': round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), 'shape': shape}
+    def run_graph(fn, n, replays=5):
+        """Per-launch time of n launches captured as one HIP graph, the way a
+        decode step replays them: median over replays of (replay time / n)."""
+        side = torch.cuda.Stream()
+        with torch.cuda.stream(side):
+            fn(0)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn(i)
+        g.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(replays):
+            ev = make_events(2)
+            ev[0].record()
+            g.replay()
+            ev[1].record()
+            torch.cuda.synchronize()
+            ts.append(ev[0].elapsed_time(ev[1]) * 1e3 / n)
+        return sorted(ts)[replays // 2]
 
-    out = {}
+    def hbm(us, nbytes, shape, graph_us=None):
+        r = {'avg_us': round(us, 2), 'bytes_per_launch': nbytes,
+             'gbs': round(nbytes / us / 1e3, 1),
+             'hbm_frac': round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), 'shape': shape}
+        if graph_us is not None:
+            r['graph_us'] = round(graph_us, 2)
+            r['graph_hbm_frac'] = round(nbytes / graph_us / 1e3 / HBM_PEAK_GBS, 4)
+        return r
+
+    # The floor of both timings: a one-element fill, timed the same two ways.
+    one = torch.empty(1, device=dev)
+    out = {'launch_floor': {'avg_us': round(run(lambda i: one.fill_(1.0), reps), 2),
+                            'graph_us': round(run_graph(lambda i: one.fill_(1.0), 64), 2),
+                            'shape': 'torch fill_ of one fp32 element'}}
     w = torch.randn((4096, H), generator=gen, device=dev) * 0.02
     q, s = quantize_g128(w)
     del w
@@ -211,9 +246,9 @@ def isolated_probe(dev, spin_cycles, reps=32):
     qp = q.unsqueeze(0).expand(pool, -1, -1).contiguous()
     sp = s.unsqueeze(0).expand(pool, -1, -1).contiguous()
     x1 = torch.randn((1, H), generator=gen, device=dev).to(torch.bfloat16)
-    us = run(lambda i: int8.linear(x1, qp[i % pool], sp[i % pool]), reps)
-    out['w8a16_linear_m1'] = hbm(us, 4096 * H + 4096 * (H // 128) * 4 + H * 2 + 4096 * 2,
-                                 '[1, 2048] x [4096, 2048] int8 g128')
+    fn1 = lambda i: int8.linear(x1, qp[i % pool], sp[i % pool])
+    out['w8a16_linear_m1'] = hbm(run(fn1, reps), 4096 * H + 4096 * (H // 128) * 4 + H * 2 + 4096 * 2,
+                                 '[1, 2048] x [4096, 2048] int8 g128', run_graph(fn1, 64))
     del qp, sp
     x2 = torch.randn((CHUNK, H), generator=gen, device=dev).to(torch.bfloat16)
     flops = 2.0 * CHUNK * 4096 * H
@@ -234,9 +269,10 @@ def isolated_probe(dev, spin_cycles, reps=32):
     s2p = s2.unsqueeze(0).expand(pool, -1, -1).contiguous()
     for m in (1, 4, 8):
         xm = torch.randn((m, H), generator=gen, device=dev).to(torch.bfloat16)
-        us = run(lambda i: w8a8.linear(xm, q2p[i % pool], s2p[i % pool], swiglu=True), reps)
+        fnm = lambda i: w8a8.linear(xm, q2p[i % pool], s2p[i % pool], swiglu=True)
         out[f'w8a8_gate_up_swiglu_m{m}'] = hbm(
-            us, GU_EXPERT_BYTES + H * 2 * m + I * 2 * m, f'[{m}, 2048] x [1024, 2048] int8 g128')
+            run(fnm, reps), GU_EXPERT_BYTES + H * 2 * m + I * 2 * m,
+            f'[{m}, 2048] x [1024, 2048] int8 g128', run_graph(fnm, 64))
     return out
 
 
