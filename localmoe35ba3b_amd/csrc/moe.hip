@@ -1037,41 +1037,18 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
     rpos[r] = p;
   }
   if (blockIdx.x != 0) return;
-  // Tile table, longest tiles first (the GEMMs dispatch workgroups in table
-  // order, and a tile's time grows with its rows, so the grid drains on the
-  // shortest): the shared expert's nst full tiles over rows [R, R + T), the
-  // routed experts' full kBM-row tiles (by expert id), then each routed
-  // expert's last partial tile, by descending rows (ties by expert id).
-  // Rows past the last tile up to nst + max_tiles are (0, 0, 0).
+  // Tile table: the shared expert's nst full tiles over rows [R, R + T)
+  // first (the longest tiles start first), then thread e writes the tiles of
+  // routed expert e at nst + its exclusive tile prefix, and rows past the
+  // last tile up to nst + max_tiles are (0, 0, 0).
   const int nst = (T + kBM - 1) / kBM;
-  const int nfull = t < kE ? c / kBM : 0;
-  const int rpart = t < kE ? c - nfull * kBM : 0;  // rows of expert t's partial tile (0: none)
-  int nftot = 0;
-  const int fex = scan(nfull, &nftot);
-  __shared__ __align__(16) int rp[kE];
-  if (t < kE) rp[t] = rpart;
-  __syncthreads();
-  int pex = 0, nptot = 0;  // partial tiles ahead of expert t's; all partial tiles
-#pragma unroll 4
-  for (int j = 0; j < kE; j += 4) {
-    const int4 v = *reinterpret_cast<const int4 *>(&rp[j]);
-    pex += (v.x > rpart || (v.x == rpart && j < t)) ? 1 : 0;
-    pex += (v.y > rpart || (v.y == rpart && j + 1 < t)) ? 1 : 0;
-    pex += (v.z > rpart || (v.z == rpart && j + 2 < t)) ? 1 : 0;
-    pex += (v.w > rpart || (v.w == rpart && j + 3 < t)) ? 1 : 0;
-    nptot += (v.x > 0) + (v.y > 0) + (v.z > 0) + (v.w > 0);
-  }
-  const int ntot = nftot + nptot;
-  for (int k = 0; k < nfull; ++k) {
-    const int64_t i = nst + fex + k;
+  const int nt = t < kE ? (c + kBM - 1) / kBM : 0;
+  int ntot = 0;
+  const int tex = scan(nt, &ntot);
+  for (int k = 0; k < nt; ++k) {
+    const int64_t i = nst + tex + k;
     table[i * 3] = t;
     table[i * 3 + 1] = offs[t] + (int64_t)k * kBM;
-    table[i * 3 + 2] = offs[t + 1];
-  }
-  if (rpart > 0) {
-    const int64_t i = nst + nftot + pex;
-    table[i * 3] = t;
-    table[i * 3 + 1] = offs[t] + (int64_t)nfull * kBM;
     table[i * 3 + 2] = offs[t + 1];
   }
   for (int i = nst + ntot + t; i < nst + max_tiles; i += 1024) {
