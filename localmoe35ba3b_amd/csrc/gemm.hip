@@ -467,9 +467,9 @@ __device__ __forceinline__ void barrier_raw() { asm volatile("s_barrier" ::: "me
 // waves) are staged in LDS, in a 3-slot ring loaded through registers one
 // stage ahead of their LDS write.  All loads are ordinary compiler-tracked
 // loads, so every wait the compiler inserts is exact.  Within a stage the
-// dequantization of the next 8-K piece is interleaved with the MFMAs of the
-// current one (one MFMA, then a few VALU ops), so a wave keeps the matrix
-// pipe and the VALU busy together.
+// next 8-K piece is dequantized while the MFMAs of the current one run (the
+// two are independent, and the compiler interleaves them), so a wave keeps
+// the matrix pipe and the VALU busy together.
 //
 // K order inside a 64-K stage: in the MFMA layout lane l (quarter q = l >> 4)
 // holds 16 consecutive weights k = 16 q .. 16 q + 15 of column l & 15; MFMA
@@ -687,7 +687,6 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   barrier_raw();
   rb_perm(0);
   dq(0, 0, 0, bcur);
-  constexpr int VG = (20 * NI + MS * NI - 1) / (MS * NI);  // dequant VALU per MFMA
   auto step = [&](int s, int ub, int ua, bool st_a, bool ld_a, bool ld_b, bool has_next) {
     if (st_a) store_a(ua, s + 1);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
@@ -719,13 +718,6 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni)
           acc[mi][ni] = T::mfma16x16x32(af[mi], bcur[ni], acc[mi][ni]);
-      __builtin_amdgcn_sched_group_barrier(0x100, MS, 0);
-      if (nxt) __builtin_amdgcn_sched_group_barrier(0x002, 2 * VG, 0);
-#pragma unroll
-      for (int i = 0; i < MS * NI; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (nxt) __builtin_amdgcn_sched_group_barrier(0x002, VG, 0);
-      }
       __builtin_amdgcn_sched_barrier(0);
       if (nxt) {
 #pragma unroll
