@@ -188,6 +188,11 @@ __device__ __forceinline__ V ldg(const void *p) {
   return *(const __attribute__((address_space(1))) V *)p;
 }
 __device__ __forceinline__ u32x4 ldg16(const void *p) { return ldg<u32x4>(p); }
+// Non-temporal 16-byte load, for data read once: it streams past the caches
+// instead of evicting data that is read again.
+__device__ __forceinline__ u32x4 ldg16_nt(const void *p) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4 *)p);
+}
 __device__ __forceinline__ float ldg_f32(const float *p) { return ldg<float>(p); }
 __device__ __forceinline__ uint2 ldg_u2(const void *p) {
   typedef unsigned u32x2 __attribute__((ext_vector_type(2)));

@@ -618,13 +618,21 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
                 (uint32_t)__builtin_amdgcn_ds_bpermute(perm_src, (int)breg[slot][ni][h][j]);
     }
   };
+  // Tile-layout weights of a tile of at most 80 rows (MS < 6; a routed
+  // expert's only tile, typically) are read by this tile alone: non-temporal
+  // loads stream them past the caches, which both raises the read rate and
+  // leaves the caches to the activation rows and the next kernel's inputs.
+  // Fuller tiles (the shared expert's, a hot expert's) keep cached loads, as
+  // other row tiles of the same expert re-read their weights.
+  constexpr bool NTW = WL == kWlTiles && MS < 6;
   auto load_b = [&](int slot, int s) {
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
-      for (int h = 0; h < HL; ++h)
-        breg[slot][ni][h] = ldg16(bsrc[ni] + (WL == kWlTiles ? (s * HL + h) * 1024
-                                                             : s * KS + 64 * h));
+      for (int h = 0; h < HL; ++h) {
+        const int8_t *p = bsrc[ni] + (WL == kWlTiles ? (s * HL + h) * 1024 : s * KS + 64 * h);
+        breg[slot][ni][h] = NTW ? ldg16_nt(p) : ldg16(p);
+      }
   };
   auto load_a = [&](int slot, int s) {
 #pragma unroll
