@@ -29,7 +29,10 @@ struct RowMap {
 // Walks this wave's instructions in batches of LOADS.  `body(w, r, g, f, ok)`
 // receives each lane's 16 bytes of row r, group g (flattened index f); ok is
 // false for lanes past the end (their w is zero).  All lanes of the wave
-// call body together, so body may use cross-lane DPP.
+// call body together, so body may use cross-lane DPP.  Weight rows are read
+// once per call and not again before the rest of a decode step's weights
+// (far more than the caches hold) have passed, so they are loaded
+// non-temporally: the loads stream past the caches, which reads HBM faster.
 template <int LOADS, typename RowPtr, typename Body>
 __device__ __forceinline__ void stream_rows(int R, int G, RowPtr row_ptr, Body body) {
   const int lane = threadIdx.x & 63;
@@ -56,7 +59,7 @@ __device__ __forceinline__ void stream_rows(int R, int G, RowPtr row_ptr, Body b
       gs[u] = g;
       fs[u] = f;
       if (ok[u]) {
-        w[u] = ldg16(row_ptr(r) + g * 128 + sub * 16);
+        w[u] = ldg16_nt(row_ptr(r) + g * 128 + sub * 16);
       } else {
         w[u] = u32x4{0u, 0u, 0u, 0u};
       }
@@ -109,7 +112,7 @@ struct RowLoads {
       r[u] = ok[u] ? rr : 0;
       g[u] = ok[u] ? gg : 0;
       f[u] = ok[u] ? ff : 0;
-      w[u] = ldg16(row_ptr(r[u]) + g[u] * 128 + sub * 16);
+      w[u] = ldg16_nt(row_ptr(r[u]) + g[u] * 128 + sub * 16);
       ff += 8;
       gg += 8;
       while (gg >= G) {
