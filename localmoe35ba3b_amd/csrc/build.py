@@ -24,6 +24,11 @@ ARCH = os.environ.get('LM_OFFLOAD_ARCH', 'gfx950')
 COMMON = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}', '-ffp-contract=off',
           '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
           '-Wno-unused-command-line-argument']
+# Per-source flags.  moe.hip: kernel-argument preloading of each kernel's
+# leading scalar arguments (up to 6) into SGPRs at launch; the decode kernels
+# take the pointers their first loads need as such arguments.  The compiler
+# emits a prologue that loads them normally for firmware without preloading.
+EXTRA = {'moe.hip': ['-mllvm', '-amdgpu-kernarg-preload-count=6']}
 
 
 def hipcc():
@@ -34,7 +39,8 @@ def hipcc():
 
 
 def _compile(src, obj):
-    cmd = [hipcc(), *COMMON, '-I', str(INCLUDE), '-c', str(src), '-o', str(obj)]
+    cmd = [hipcc(), *COMMON, *EXTRA.get(src.name, []), '-I', str(INCLUDE), '-c', str(src), '-o',
+           str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "'-packed-fp32-ops' is not a recognized feature"
     err = '\n'.join(l for l in proc.stderr.splitlines() if noise not in l)
