@@ -617,7 +617,16 @@ __global__ __launch_bounds__(256) void decode_down_kernel(int *p_sel, uint16_t *
 // RMSNorm of each token row + the shared-expert gate logit (fp64 dot) + the
 // Euclidean norms that bound the approximate router logits: |xn| of each
 // token (workgroups < T) and |w_e| of each router row (workgroups < kE).
-__global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a, int T) {
+// Leading pointer arguments: preloaded into SGPRs at launch, as in the decode
+// kernels.
+__global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, const uint16_t *p_router_w,
+                                                                const uint16_t *p_gate_w,
+                                                                const float *p_norm_w, int T,
+                                                                LayerArgs a) {
+  a.h = p_h;
+  a.router_w = p_router_w;
+  a.gate_w = p_gate_w;
+  a.norm_w = p_norm_w;
   __shared__ float xf[kH];
   __shared__ float red[4];
   __shared__ float red2[4];
@@ -693,7 +702,10 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(LayerArgs a, int
 // prefill_topk_count_kernel bounds the error of any order.
 constexpr int kRaTok = 32, kRaExp = 64;
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void
-router_approx_kernel(LayerArgs a, int T) {
+router_approx_kernel(uint16_t *p_xn, const uint16_t *p_router_w, float *p_logits, int T, LayerArgs a) {
+  a.xn = p_xn;
+  a.router_w = p_router_w;
+  a.logits = p_logits;
   constexpr int KQ = kH / 4;
   constexpr int SS = 128, NSS = KQ / SS, PITCH = 272;
   constexpr int NLD = (kRaTok + kRaExp) / 4;  // wave loads per segment: 8 token + 16 expert
@@ -939,9 +951,14 @@ constexpr int kScanRoutes = 1024;  // routes per prefill_scan_kernel workgroup
 constexpr int kScanGroups = kScanRoutes / (kTopkTokens * kTopK);  // top-k workgroups per scan one
 static_assert(kScanGroups * kTopkTokens * kTopK == kScanRoutes, "scan slices whole top-k groups");
 
-__global__ __launch_bounds__(kTopkTokens * 64) void prefill_topk_count_kernel(LayerArgs a, int T,
-                                                                             uint8_t *bcounts,
-                                                                             int *rslot) {
+__global__ __launch_bounds__(kTopkTokens * 64) void prefill_topk_count_kernel(
+    int T, const float *p_router_bias, uint16_t *p_xn, float *p_logits, float *p_nw, float *p_nx,
+    LayerArgs a, uint8_t *bcounts, int *rslot) {
+  a.router_bias = p_router_bias;
+  a.xn = p_xn;
+  a.logits = p_logits;
+  a.nw = p_nw;
+  a.nx = p_nx;
   __shared__ int lcnt[kE];
   __shared__ int64_t sid[kTopkTokens][kTopK];
   __shared__ uint16_t swt[kTopkTokens][kTopK];
@@ -1095,8 +1112,11 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
 
 // Per token: routed combine in ascending expert order, gated shared add,
 // residual add (in place on h).  256 threads x 8 columns.
-__global__ __launch_bounds__(256) void prefill_combine_kernel(LayerArgs a, const int *rpos,
-                                                              const uint16_t *vbuf, int64_t R) {
+__global__ __launch_bounds__(256) void prefill_combine_kernel(int64_t *p_ids, const int *rpos,
+                                                              uint16_t *p_wts, const uint16_t *vbuf,
+                                                              int64_t R, LayerArgs a) {
+  a.ids = p_ids;
+  a.wts = p_wts;
   const int tok = blockIdx.x;
   const int c = threadIdx.x * 8;
   int e[kTopK], p[kTopK];
@@ -1318,14 +1338,17 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   int *rpos = reinterpret_cast<int *>(ws + w.rpos);
   uint16_t *vbuf = reinterpret_cast<uint16_t *>(ws + w.vbuf);
   if (int rc = mark(0)) return rc;
-  prefill_norm_gate_kernel<<<(unsigned)(T > kE ? T : kE), 256, 0, st>>>(a, (int)T);
+  prefill_norm_gate_kernel<<<(unsigned)(T > kE ? T : kE), 256, 0, st>>>(a.h, a.router_w, a.gate_w,
+                                                                    a.norm_w, (int)T, a);
   if (int rc = check_launch("prefill_norm_gate_kernel")) return rc;
   if (int rc = mark(1)) return rc;
-  router_approx_kernel<<<dim3(cdiv(T, kRaTok), kE / kRaExp), 256, 0, st>>>(a, (int)T);
+  router_approx_kernel<<<dim3(cdiv(T, kRaTok), kE / kRaExp), 256, 0, st>>>(a.xn, a.router_w,
+                                                                          a.logits, (int)T, a);
   if (int rc = check_launch("router_approx_kernel")) return rc;
   if (int rc = mark(2)) return rc;
   const int nb = (int)cdiv(T, kTopkTokens);
-  prefill_topk_count_kernel<<<nb, kTopkTokens * 64, 0, st>>>(a, (int)T, bcounts, rslot);
+  prefill_topk_count_kernel<<<nb, kTopkTokens * 64, 0, st>>>((int)T, a.router_bias, a.xn, a.logits,
+                                                              a.nw, a.nx, a, bcounts, rslot);
   if (int rc = check_launch("prefill_topk_count_kernel")) return rc;
   if (int rc = mark(3)) return rc;
   prefill_scan_kernel<<<cdiv(R, kScanRoutes), 1024, 0, st>>>(a.ids, rslot, bcounts, nb, (int)T,
@@ -1345,7 +1368,7 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
                       kH,      kI,      false, false,  LM_BF16, layer->dn_q_tiles};
   if (int rc = routed_gemm(dn, st)) return rc;
   if (int rc = mark(6)) return rc;
-  prefill_combine_kernel<<<(unsigned)T, 256, 0, st>>>(a, rpos, vbuf, R);
+  prefill_combine_kernel<<<(unsigned)T, 256, 0, st>>>(a.ids, rpos, a.wts, vbuf, R, a);
   if (int rc = check_launch("prefill_combine_kernel")) return rc;
   if (int rc = mark(7)) return rc;
   if (ids_out || weights_out) {
