@@ -322,15 +322,18 @@ __device__ __forceinline__ uint32_t lane_xor_u32(uint32_t v) {
   }
 }
 // Lane l's copy of lane l ^ M for the mirror partners of the top-8 merges:
-// 15 (row mirror), 23 (swizzle within 32 lanes), 39 (permute across the wave).
+// 7 (half-row mirror), 15 (row mirror), 23 (swizzle within 32 lanes), 39
+// (permute across the wave).
 template <int M>
 __device__ __forceinline__ uint32_t lane_mirror_u32(uint32_t v) {
-  if constexpr (M == 15) {
+  if constexpr (M == 7) {
+    return dpp_u32<0x141>(v);
+  } else if constexpr (M == 15) {
     return dpp_u32<0x140>(v);
   } else if constexpr (M == 23) {
     return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (23 << 10) | 0x1F);
   } else {
-    static_assert(M == 39, "lane_mirror_u32: M in {15, 23, 39}");
+    static_assert(M == 39, "lane_mirror_u32: M in {7, 15, 23, 39}");
     return (uint32_t)__shfl_xor((int)v, 39, 64);
   }
 }
@@ -388,6 +391,33 @@ __device__ __forceinline__ T wave_top8(T k, int lane) {
   k = merge_top8<15>(k, lane);
   k = merge_top8<23>(k, lane);
   return merge_top8<39>(k, lane);
+}
+// Two lists per 8-lane block, each sorted descending -> the 8 largest of
+// both, sorted descending (b is read mirrored within the block, as in
+// merge_top8).
+template <typename T>
+__device__ __forceinline__ T merge2_top8(T a, T b, int lane) {
+  const T p = lane_mirror<7>(b);
+  T k = a > p ? a : p;
+  k = lane_cx<4>(k, lane, true);
+  k = lane_cx<2>(k, lane, true);
+  return lane_cx<1>(k, lane, true);
+}
+// The 8th largest of the wave's 256 keys (4 per lane, distinct), in every
+// lane, by DPP exchanges alone: each key slot is sorted within its 8-lane
+// blocks, the four sorted slots are merged within each block (its top 8 of
+// 32), then the blocks are merged across the wave as in wave_top8.
+template <class KT>
+__device__ __forceinline__ typename KT::T kth8_key_wave(const typename KT::T key[4], int lane) {
+  using T = typename KT::T;
+  T s[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s[j] = sort8_desc(key[j], lane);
+  T k = merge2_top8(merge2_top8(s[0], s[1], lane), merge2_top8(s[2], s[3], lane), lane);
+  k = merge_top8<15>(k, lane);
+  k = merge_top8<23>(k, lane);
+  k = merge_top8<39>(k, lane);
+  return KT::readlane(k, 7);
 }
 
 // LDS scratch of one top-k wave, in 64-bit words: 4 rows x 16 candidates
@@ -454,23 +484,6 @@ __device__ __forceinline__ int topk_winner_rank(const typename KT::T *scratch, i
 #pragma unroll 8
   for (int j = 0; j < nc; ++j) rank += scratch[j] > mine ? 1 : 0;
   return rank;
-}
-
-// The K-th largest of the wave's 256 keys (4 per lane), in every lane.
-template <class KT>
-__device__ __forceinline__ typename KT::T kth_key_wave(typename KT::T key[4], int K, int lane,
-                                                      unsigned long long *scratch_words) {
-  using T = typename KT::T;
-  T *scratch = reinterpret_cast<T *>(scratch_words);
-  topk_row_winners<KT>(key, K, lane, scratch);
-  wave_lds_sync();
-  T mine;
-  const int rank = topk_winner_rank<KT>(scratch, K, lane, mine);
-  wave_lds_sync();
-  T *out = reinterpret_cast<T *>(scratch_words + 64);
-  if (lane < 4 * K && rank == K - 1) out[0] = mine;
-  wave_lds_sync();
-  return out[0];
 }
 
 template <class KT>

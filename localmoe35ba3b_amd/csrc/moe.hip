@@ -833,7 +833,8 @@ __device__ void topk_exact_wave(const LayerArgs &a, int tok, int lane, unsigned 
     klo[j] = KT::make(lo[j], e);
     khi[j] = KT::make(hi[j], e);
   }
-  const T t8 = kth_key_wave<KT>(klo, kTopK, lane, scratch);
+  static_assert(kTopK == 8, "T8 is the 8th largest lower-bound key");
+  const T t8 = kth8_key_wave<KT>(klo, lane);
   // candidates, compacted into cand[0 .. n)
   int n = 0;
 #pragma unroll
