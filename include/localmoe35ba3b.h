@@ -262,6 +262,10 @@ int lm_rmsnorm(const void *x, const float *w, void *y, int64_t rows,
  * matter (lm_moe_workspace_init zeroes all of it for callers that want a
  * defined state).  Calls sharing a workspace must not overlap. */
 typedef struct lm_moe_layer {
+  /* sizeof(lm_moe_layer) as the caller compiled it; calls refuse any other
+   * value (LM_EINVAL), so a caller built against an older layout of this
+   * struct is rejected instead of misread. */
+  int64_t struct_size;
   const void *router_w;
   const float *router_bias;
   const void *shared_gate_w;
@@ -288,18 +292,30 @@ int64_t lm_moe_workspace_bytes(int64_t max_tokens, int64_t hidden,
                                int64_t inter, int64_t experts, int64_t top_k);
 int lm_moe_workspace_init(void *workspace, int64_t bytes, void *stream);
 
-/* Where a prefill call (tokens > 1) on `tokens` rows leaves its
- * intermediates in the workspace: byte offset and size of one region, for
- * tests and debugging (no reference counterpart; the reference keeps these
- * in separate torch tensors, prefill.py:52-85).  Regions:
+/* Where a call on `tokens` rows leaves its intermediates in the workspace:
+ * byte offset and size of one region, for tests and debugging (no
+ * reference counterpart; the reference keeps these in separate torch
+ * tensors, prefill.py:52-85, int8.py:155-210).  R = tokens * top_k.
+ * Regions of every call:
  *   LM_WS_NORMED      bf16  [tokens, H]      RMSNorm output (router input)
  *   LM_WS_GATE        fp32  [tokens]         shared-expert gate logits
  *   LM_WS_IDS         int64 [tokens, top_k]  selected experts, selection order
  *   LM_WS_WEIGHTS     bf16  [tokens, top_k]  routing weights, same order
- *   LM_WS_ROUTE_ROWS  int32 [tokens, top_k]  expert-sorted row of each route
  *   LM_WS_HIDDEN      bf16  [R + tokens, I]  SwiGLU rows (routed, then shared)
  *   LM_WS_DOWN        bf16  [R + tokens, H]  down rows (routed, then shared)
- * with R = tokens * top_k.  Valid until the next call using the workspace. */
+ * of prefill calls (tokens > 1) only:
+ *   LM_WS_ROUTE_ROWS  int32 [tokens, top_k]  expert-sorted row of each route
+ * of decode calls (tokens == 1) only, whose routed rows in LM_WS_HIDDEN and
+ * LM_WS_DOWN are in combine order (ascending expert id, slot s = row s):
+ *   LM_WS_ACT_Q       int8  [H]              w8a8.quantize of the normed row
+ *   LM_WS_ACT_SCALES  fp32  [H/128]          its group scales
+ *   LM_WS_SLOT_IDS    int32 [top_k]          expert of each combine slot
+ *   LM_WS_SLOT_WEIGHTS fp32 [top_k]          its (bf16-valued) routing weight
+ *   LM_WS_GATE_UP_ACC fp32  [top_k, 2I]      W8A8 epilogue sums of the routed
+ *                                            gate_up rows (w8a8.py:40), before
+ *                                            the bf16 rounding
+ *   LM_WS_DOWN_ACC    fp32  [top_k, H]       the same for the down rows
+ * Valid until the next call using the workspace. */
 #define LM_WS_NORMED 0
 #define LM_WS_GATE 1
 #define LM_WS_IDS 2
@@ -307,6 +323,12 @@ int lm_moe_workspace_init(void *workspace, int64_t bytes, void *stream);
 #define LM_WS_ROUTE_ROWS 4
 #define LM_WS_HIDDEN 5
 #define LM_WS_DOWN 6
+#define LM_WS_ACT_Q 7
+#define LM_WS_ACT_SCALES 8
+#define LM_WS_SLOT_IDS 9
+#define LM_WS_SLOT_WEIGHTS 10
+#define LM_WS_GATE_UP_ACC 11
+#define LM_WS_DOWN_ACC 12
 int lm_moe_workspace_region(int64_t tokens, int region, int64_t *offset,
                             int64_t *bytes);
 
@@ -327,14 +349,23 @@ int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t tokens,
 /* lm_moe_layer_forward without a workspace argument: the call's workspace
  * is a device array inside the library (one per device, about 6.6 MB, held
  * until the process ends), so the call allocates nothing and takes no
- * scratch from the caller.  No counterpart in the reference: it is for
- * callers that cannot allocate device memory - code under HIP graph
- * capture, tight serving loops, harnesses that forbid hipMalloc.  At most
+ * scratch from the caller.  It may be captured in a HIP graph once
+ * lm_moe_static_init() has run on the device.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory - code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  At most
  * lm_moe_static_max_tokens() (128) tokens per call (LM_ENOMEM beyond);
  * same results as lm_moe_layer_forward.  Every call on one device shares
  * that device's array: calls that overlap on a device (several streams or
  * host threads) race and must be serialized by the caller. */
 int64_t lm_moe_static_max_tokens(void);
+/* Resolves the device array of lm_moe_layer_forward_static on the current
+ * device (once per device; later calls return at once).  Call it before
+ * capturing static calls in a HIP graph: a static call on a device whose
+ * array is not resolved yet resolves it itself when its stream is not
+ * capturing, and is refused (LM_EINVAL) when it is.  The stream of a static
+ * call must belong to the current device (LM_EINVAL otherwise). */
+int lm_moe_static_init(void);
 int lm_moe_layer_forward_static(const lm_moe_layer *layer, void *h,
                                 int64_t tokens, int64_t hidden, int64_t inter,
                                 int64_t experts, int64_t top_k, float eps,

@@ -16,7 +16,8 @@ LM_OK, LM_EINVAL, LM_ENOMEM, LM_ELAUNCH = 0, 1, 2, 3
 LM_BF16, LM_FP16, LM_FP32 = 0, 1, 2
 # fused-layer workspace regions (lm_moe_workspace_region)
 WS_REGIONS = {'normed': 0, 'gate': 1, 'ids': 2, 'weights': 3, 'route_rows': 4, 'hidden': 5,
-              'down': 6}
+              'down': 6, 'act_q': 7, 'act_scales': 8, 'slot_ids': 9, 'slot_weights': 10,
+              'gate_up_acc': 11, 'down_acc': 12}
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64
@@ -54,17 +55,23 @@ SIGNATURES = {
     'lm_moe_workspace_region': (I32, [I64, I32, P, P]),
     'lm_moe_layer_forward': (I32, [P, P, I64, I64, I64, I64, I64, F32, P, I64, P, P, P, P]),
     'lm_moe_static_max_tokens': (I64, []),
+    'lm_moe_static_init': (I32, []),
     'lm_moe_layer_forward_static': (I32, [P, P, I64, I64, I64, I64, I64, F32, P, P, P, P]),
 }
 
 
 class MoeLayer(ctypes.Structure):
-    """struct lm_moe_layer."""
-    _fields_ = [('router_w', P), ('router_bias', P), ('shared_gate_w', P), ('norm_w', P),
+    """struct lm_moe_layer.  struct_size is filled in on construction;
+    positional arguments start at router_w."""
+    _fields_ = [('struct_size', I64),
+                ('router_w', P), ('router_bias', P), ('shared_gate_w', P), ('norm_w', P),
                 ('gu_q', P), ('gu_s', P), ('dn_q', P), ('dn_s', P),
                 ('gu_q_expert_stride', I64), ('gu_s_expert_stride', I64),
                 ('dn_q_expert_stride', I64), ('dn_s_expert_stride', I64),
                 ('gu_q_tiles', P), ('dn_q_tiles', P)]
+
+    def __init__(self, *args, **kw):
+        super().__init__(ctypes.sizeof(MoeLayer), *args, **kw)
 
 
 _lib = None

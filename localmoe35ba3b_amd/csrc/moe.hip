@@ -35,8 +35,8 @@ constexpr int kTopkTokens = 8;  // prefill top-k: tokens (waves) per workgroup
 static_assert(kE == 256, "the prefill kernels map one thread of a 256-thread workgroup to each expert");
 
 struct WsLayout {
-  int64_t bcounts, xn, gl, logits, nx, nw, ids, wts, sel, selw, xq, xs, pos, table, rslot,
-      rpos, hbuf, vbuf, total;
+  int64_t bcounts, xn, gl, logits, nx, nw, ids, wts, sel, selw, xq, xs, dacc_gu, dacc_dn, pos,
+      table, rslot, rpos, hbuf, vbuf, total;
   int64_t max_tiles, n_tiles;
 };
 
@@ -64,6 +64,8 @@ constexpr WsLayout layout(int64_t T) {
   w.selw = take(kTopK * 4);
   w.xq = take(kH);
   w.xs = take(kH / 128 * 4);
+  w.dacc_gu = take(kTopK * 2 * kI * 4);  // decode: fp32 W8A8 sums of the routed gate_up rows
+  w.dacc_dn = take(kTopK * kH * 4);      // decode: fp32 W8A8 sums of the routed down rows
   w.pos = take((R + T) * 8);
   w.table = take(w.n_tiles * 3 * 8);
   w.bcounts = take((T + kTopkTokens - 1) / kTopkTokens * kE);  // per top-k workgroup expert counts (bytes)
@@ -100,6 +102,9 @@ struct LayerArgs {
   int8_t *xq;
   float *xs;
   uint16_t *hbuf;
+  uint16_t *vbuf;   // decode: the 8 routed down rows (bf16) and the shared one
+  float *dacc_gu;   // decode: fp32 epilogue sums of the routed gate_up rows [8, 2I]
+  float *dacc_dn;   // decode: fp32 epilogue sums of the routed down rows [8, H]
   int32_t *ids_out;
   uint16_t *wts_out;
 };
@@ -437,6 +442,9 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(float *p_logits, in
     }
     const float gate = round_bf16(sg), up = round_bf16(su);
     a.hbuf[slot * kI + n0 + t] = f32_to_bf16_bits(round_bf16(silu_f32(gate)) * up);
+    // the fp32 epilogue sums, before the bf16 rounding of w8a8.py:41
+    a.dacc_gu[slot * 2 * kI + n0 + t] = sg;
+    a.dacc_gu[slot * 2 * kI + kI + n0 + t] = su;
   } else if (t == 64) {  // the shared column, from the terms of all four waves
     float sg = 0.0f, su = 0.0f;
     for (int g = 0; g < G; ++g) {
@@ -598,10 +606,17 @@ __global__ __launch_bounds__(256) void decode_down_kernel(int *p_sel, uint16_t *
     const int c = t & (kDnCols - 1);
     float v8 = 0.0f;
     for (int g = 0; g < G; ++g) v8 = add_rn(v8, term[t * G + g]);
-    prod[t] = round_bf16(round_bf16(v8) * selw[t / kDnCols]);
+    const float vr = round_bf16(v8);
+    prod[t] = round_bf16(vr * selw[t / kDnCols]);
     float vs = 0.0f;
     for (int g = 0; g < G; ++g) vs += term[(RR + c) * G + g];
     const float shared = round_bf16(round_bf16(sigmoid_f32(glv)) * round_bf16(vs));
+    // The layer's intermediates stay in the workspace: slot s's down row
+    // (bf16 and its fp32 epilogue sum) and, from lanes 0 .. 7, the shared one.
+    const int s = t / kDnCols;
+    a.vbuf[s * kH + c0 + c] = f32_to_bf16_bits(vr);
+    a.dacc_dn[s * kH + c0 + c] = v8;
+    if (t < kDnCols) a.vbuf[kTopK * kH + c0 + c] = f32_to_bf16_bits(vs);
     wave_lds_sync();
     if (t < kDnCols) {
       float acc = 0.0f;
@@ -1203,14 +1218,33 @@ extern "C" int lm_moe_workspace_region(int64_t tokens, int region, int64_t *offs
   LM_REQUIRE(offset && bytes, LM_EINVAL, "null pointer");
   const WsLayout w = layout(tokens);
   const int64_t T = tokens, R = T * kTopK;
+  const bool decode = T == 1;
   switch (region) {
     case LM_WS_NORMED: *offset = w.xn; *bytes = T * kH * 2; break;
     case LM_WS_GATE: *offset = w.gl; *bytes = T * 4; break;
     case LM_WS_IDS: *offset = w.ids; *bytes = R * 8; break;
     case LM_WS_WEIGHTS: *offset = w.wts; *bytes = R * 2; break;
-    case LM_WS_ROUTE_ROWS: *offset = w.rpos; *bytes = R * 4; break;
+    case LM_WS_ROUTE_ROWS:
+      LM_REQUIRE(!decode, LM_EINVAL, "a decode call has no route rows");
+      *offset = w.rpos; *bytes = R * 4; break;
     case LM_WS_HIDDEN: *offset = w.hbuf; *bytes = (R + T) * kI * 2; break;
     case LM_WS_DOWN: *offset = w.vbuf; *bytes = (R + T) * kH * 2; break;
+    case LM_WS_ACT_Q:
+    case LM_WS_ACT_SCALES:
+    case LM_WS_SLOT_IDS:
+    case LM_WS_SLOT_WEIGHTS:
+    case LM_WS_GATE_UP_ACC:
+    case LM_WS_DOWN_ACC:
+      LM_REQUIRE(decode, LM_EINVAL, "region written by decode calls (one token) only");
+      switch (region) {
+        case LM_WS_ACT_Q: *offset = w.xq; *bytes = kH; break;
+        case LM_WS_ACT_SCALES: *offset = w.xs; *bytes = kH / 128 * 4; break;
+        case LM_WS_SLOT_IDS: *offset = w.sel; *bytes = kTopK * 4; break;
+        case LM_WS_SLOT_WEIGHTS: *offset = w.selw; *bytes = kTopK * 4; break;
+        case LM_WS_GATE_UP_ACC: *offset = w.dacc_gu; *bytes = kTopK * 2 * kI * 4; break;
+        default: *offset = w.dacc_dn; *bytes = kTopK * kH * 4; break;
+      }
+      break;
     default: return set_error(LM_EINVAL, "unknown workspace region");
   }
   return LM_OK;
@@ -1230,12 +1264,13 @@ extern "C" int lm_moe_workspace_init(void *workspace, int64_t bytes, void *strea
 // tokens lives in a file-scope device array.  Each device that runs the
 // library holds its own copy until the process ends; its address on a
 // device comes from hipGetSymbolAddress, taken once per device (with that
-// device current) on the first call there and kept.  Every call on a device
-// shares that device's array, so calls that overlap on one device (other
-// streams, other host threads) race.  No region needs a starting value:
-// every call writes each region before reading it.
+// device current) by lm_moe_static_init or, outside graph capture, by the
+// first static call there, and kept.  Every call on a device shares that
+// device's array, so calls that overlap on one device (other streams, other
+// host threads) race.  No region needs a starting value: every call writes
+// each region before reading it.
 constexpr int64_t kScratchMaxTokens = 128;
-constexpr int64_t kScratchBytes = layout(kScratchMaxTokens).total;  // about 6.6 MB
+constexpr int64_t kScratchBytes = layout(kScratchMaxTokens).total;  // about 6.7 MB
 __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
@@ -1243,16 +1278,25 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void *g_scratch_ptr[kMaxDevices] = {};
 
-int device_scratch(void **ptr) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
+int current_device(int *dev) {
+  hipError_t e = hipGetDevice(dev);
   if (e != hipSuccess)
     return set_error(LM_ELAUNCH, std::string("hipGetDevice failed: ") + hipGetErrorString(e));
-  LM_REQUIRE(dev >= 0 && dev < kMaxDevices, LM_EINVAL, "device index beyond 63");
+  LM_REQUIRE(*dev >= 0 && *dev < kMaxDevices, LM_EINVAL, "device index beyond 63");
+  return LM_OK;
+}
+
+// The scratch address on device `dev` (the current device), resolved on
+// first use unless `capturing`: the lookup is not a stream operation, but it
+// is kept out of graph capture, where only stream work belongs.
+int device_scratch(int dev, bool capturing, void **ptr) {
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (!g_scratch_ptr[dev]) {
+    LM_REQUIRE(!capturing, LM_EINVAL,
+               "the static scratch of this device is not resolved: call lm_moe_static_init() "
+               "before capturing lm_moe_layer_forward_static");
     void *p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
       return set_error(LM_ELAUNCH, std::string("hipGetSymbolAddress(scratch) failed: ") +
                                        hipGetErrorString(e));
@@ -1272,6 +1316,9 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
              "fused MoE layer supports hidden 2048, intermediate 512, 256 experts, top-8");
   LM_REQUIRE(tokens >= 1 && tokens <= 65536, LM_EINVAL, "invalid token count");
   LM_REQUIRE(layer && h && workspace, LM_EINVAL, "null pointer");
+  LM_REQUIRE(layer->struct_size == (int64_t)sizeof(lm_moe_layer), LM_EINVAL,
+             "lm_moe_layer.struct_size differs from this library's sizeof(lm_moe_layer): "
+             "set it, or rebuild the caller against this header");
   LM_REQUIRE(layer->router_w && layer->shared_gate_w && layer->gu_q && layer->gu_s &&
                  layer->dn_q && layer->dn_s,
              LM_EINVAL, "null layer weight");
@@ -1305,6 +1352,9 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   a.xq = reinterpret_cast<int8_t *>(ws + w.xq);
   a.xs = reinterpret_cast<float *>(ws + w.xs);
   a.hbuf = reinterpret_cast<uint16_t *>(ws + w.hbuf);
+  a.vbuf = reinterpret_cast<uint16_t *>(ws + w.vbuf);
+  a.dacc_gu = reinterpret_cast<float *>(ws + w.dacc_gu);
+  a.dacc_dn = reinterpret_cast<float *>(ws + w.dacc_dn);
   a.ids_out = ids_out;
   a.wts_out = static_cast<uint16_t *>(weights_out);
   hipStream_t st = as_stream(stream);
@@ -1337,7 +1387,7 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   uint8_t *bcounts = ws + w.bcounts;
   int *rslot = reinterpret_cast<int *>(ws + w.rslot);
   int *rpos = reinterpret_cast<int *>(ws + w.rpos);
-  uint16_t *vbuf = reinterpret_cast<uint16_t *>(ws + w.vbuf);
+  uint16_t *vbuf = a.vbuf;
   if (int rc = mark(0)) return rc;
   prefill_norm_gate_kernel<<<(unsigned)(T > kE ? T : kE), 256, 0, st>>>(a.h, a.router_w, a.gate_w,
                                                                     a.norm_w, (int)T, a);
@@ -1381,6 +1431,13 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
 
 extern "C" int64_t lm_moe_static_max_tokens(void) { return kScratchMaxTokens; }
 
+extern "C" int lm_moe_static_init(void) {
+  int dev = -1;
+  if (int rc = current_device(&dev)) return rc;
+  void *ws = nullptr;
+  return device_scratch(dev, false, &ws);
+}
+
 extern "C" int lm_moe_layer_forward_static(const lm_moe_layer *layer, void *h, int64_t tokens,
                                            int64_t hidden, int64_t inter, int64_t experts,
                                            int64_t top_k, float eps, int32_t *ids_out,
@@ -1390,8 +1447,23 @@ extern "C" int lm_moe_layer_forward_static(const lm_moe_layer *layer, void *h, i
   LM_REQUIRE(tokens <= kScratchMaxTokens, LM_ENOMEM,
              "token count exceeds the static scratch (128 tokens); use lm_moe_layer_forward "
              "with a caller workspace");
+  // The array is looked up for the current device, so the kernels must run
+  // there: a stream of another device would hand them a foreign address.
+  int dev = -1, sdev = -1;
+  if (int rc = current_device(&dev)) return rc;
+  hipStream_t st = as_stream(stream);
+  hipError_t e = hipStreamGetDevice(st, &sdev);
+  if (e != hipSuccess)
+    return set_error(LM_EINVAL, std::string("hipStreamGetDevice failed: ") + hipGetErrorString(e));
+  LM_REQUIRE(sdev == dev, LM_EINVAL,
+             "the stream belongs to another device than the current one; make the stream's "
+             "device current for lm_moe_layer_forward_static");
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(st, &cs);
+  if (e != hipSuccess)
+    return set_error(LM_EINVAL, std::string("hipStreamIsCapturing failed: ") + hipGetErrorString(e));
   void *ws = nullptr;
-  if (int rc = device_scratch(&ws)) return rc;
+  if (int rc = device_scratch(dev, cs != hipStreamCaptureStatusNone, &ws)) return rc;
   return lm_moe_layer_forward(layer, h, tokens, hidden, inter, experts, top_k, eps, ws,
                               kScratchBytes, ids_out, weights_out, phase_events, stream);
 }

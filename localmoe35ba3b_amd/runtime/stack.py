@@ -88,6 +88,8 @@ class MoEStack:
         self._structs = [self._layer_struct(l) for l in range(layers)]
         self._side = self._side_ws = None  # second stream and workspace of prefill_
         self.gu_q_tiles = self.dn_q_tiles = None  # see build_prefill_tiles
+        self._tiles_of = None  # versions of gu_q / dn_q the tile copies were built from
+        self._static_ready = False
 
     # ------------------------------------------------------------------ views
     def bank_bytes(self):
@@ -118,7 +120,19 @@ class MoEStack:
                           q.stride(1), t[l].data_ptr(), st)
             self._structs[l].gu_q_tiles = self.gu_q_tiles[l].data_ptr()
             self._structs[l].dn_q_tiles = self.dn_q_tiles[l].data_ptr()
+        self._tiles_of = self._bank_versions()
         return self
+
+    def _bank_versions(self):
+        return (self.gu_q._version, self.dn_q._version)
+
+    def check_tiles(self):
+        """Raises when gu_q or dn_q were written in place after the tile
+        copies were built: prefill would read the old weights through the
+        copies while decode reads the new ones."""
+        if self._tiles_of is not None and self._tiles_of != self._bank_versions():
+            raise RuntimeError('gu_q / dn_q changed after build_prefill_tiles(); call it again '
+                               'so that the prefill tile copies hold the same weights')
 
     def _layer_struct(self, l):
         s = _lib.MoeLayer()
@@ -157,6 +171,7 @@ class MoEStack:
         tokens = h.shape[0]
         if tokens > self.max_tokens:
             raise MemoryError('token count exceeds the workspace of this stack')
+        self.check_tiles()
         ev = None
         if events is not None:
             ev = (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
@@ -169,13 +184,18 @@ class MoEStack:
     _REGION_TYPES = {'normed': (torch.bfloat16, 'H'), 'gate': (torch.float32, None),
                      'ids': (torch.int64, 'K'), 'weights': (torch.bfloat16, 'K'),
                      'route_rows': (torch.int32, 'K'), 'hidden': (torch.bfloat16, 'I'),
-                     'down': (torch.bfloat16, 'H')}
+                     'down': (torch.bfloat16, 'H'), 'act_q': (torch.int8, None),
+                     'act_scales': (torch.float32, None), 'slot_ids': (torch.int32, None),
+                     'slot_weights': (torch.float32, None),
+                     'gate_up_acc': (torch.float32, '2I'), 'down_acc': (torch.float32, 'H')}
 
     def workspace_view(self, region, tokens, workspace=None):
-        """Typed view of one intermediate a prefill call on `tokens` rows left
-        in the workspace (lm_moe_workspace_region): 'normed', 'gate', 'ids',
-        'weights', 'route_rows', 'hidden' or 'down'.  Valid until the next
-        call that uses the same workspace."""
+        """Typed view of one intermediate a call on `tokens` rows left in the
+        workspace (lm_moe_workspace_region): 'normed', 'gate', 'ids',
+        'weights', 'hidden', 'down'; 'route_rows' of prefill calls; the W8A8
+        intermediates of decode calls 'act_q', 'act_scales', 'slot_ids',
+        'slot_weights', 'gate_up_acc', 'down_acc'.  Valid until the next call
+        that uses the same workspace."""
         ws = self.workspace if workspace is None else workspace
         off, nbytes = ctypes.c_int64(), ctypes.c_int64()
         _lib.call('lm_moe_workspace_region', tokens, _lib.WS_REGIONS[region],
@@ -184,7 +204,7 @@ class MoEStack:
         raw = ws[off.value:off.value + nbytes.value].view(dtype)
         if inner is None:
             return raw
-        return raw.view(-1, {'H': self.H, 'I': self.I, 'K': self.K}[inner])
+        return raw.view(-1, {'H': self.H, 'I': self.I, 'K': self.K, '2I': 2 * self.I}[inner])
 
     def layer_forward_static(self, h, l, ids_out=None, weights_out=None):
         """layer_forward through lm_moe_layer_forward_static: the workspace is
@@ -193,9 +213,17 @@ class MoEStack:
         overlap)."""
         if h.dtype != torch.bfloat16 or not h.is_contiguous() or h.shape[-1] != self.H:
             raise ValueError('expected contiguous bf16 [tokens, 2048] hidden states')
-        _lib.call('lm_moe_layer_forward_static', ctypes.byref(self._structs[l]), h.data_ptr(),
-                  h.shape[0], self.H, self.I, self.E, self.K, EPS, _lib.ptr(ids_out),
-                  _lib.ptr(weights_out), None, _lib.stream(h.device))
+        if h.device != self.device:
+            raise ValueError(f'hidden states on {h.device}, stack on {self.device}')
+        self.check_tiles()
+        with torch.cuda.device(h.device):
+            if not self._static_ready:
+                # resolves the library's array on this device; kept out of graph capture
+                _lib.call('lm_moe_static_init')
+                self._static_ready = True
+            _lib.call('lm_moe_layer_forward_static', ctypes.byref(self._structs[l]),
+                      h.data_ptr(), h.shape[0], self.H, self.I, self.E, self.K, EPS,
+                      _lib.ptr(ids_out), _lib.ptr(weights_out), None, _lib.stream(h.device))
         return h
 
     def forward(self, h, layers=None):

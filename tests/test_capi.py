@@ -110,6 +110,44 @@ def test_moe_layer_bounds_rejected_before_launch():
     hole = _lib.MoeLayer(*([fake] * 5), None, fake, fake, 0, 0, 0, 0)
     assert fwd(16, ws, lay=hole) == _lib.LM_EINVAL
     assert b'null layer weight' in lib.lm_last_error()
+    # a caller compiled against another layout of the struct is refused
+    assert layer.struct_size == ctypes.sizeof(_lib.MoeLayer) == 15 * 8  # the ENOMEM above: C agrees
+    older = _lib.MoeLayer(*([fake] * 8), 0, 0, 0, 0)
+    older.struct_size = ctypes.sizeof(_lib.MoeLayer) - 16
+    assert fwd(16, ws, lay=older) == _lib.LM_EINVAL
+    assert b'struct_size' in lib.lm_last_error()
+
+
+def test_workspace_regions():
+    """Every region lies inside the workspace of its token count; the
+    decode-only regions (W8A8 intermediates of the one-token path) and the
+    prefill-only route rows are refused for the other kind of call."""
+    lib = _lib.lib()
+    off, nb = ctypes.c_int64(), ctypes.c_int64()
+    for tokens in (1, 2, 37, 2048):
+        total = lib.lm_moe_workspace_bytes(tokens, 2048, 512, 256, 8)
+        spans = []
+        for name, code in _lib.WS_REGIONS.items():
+            rc = lib.lm_moe_workspace_region(tokens, code, ctypes.byref(off), ctypes.byref(nb))
+            decode_only = code >= 7
+            if (tokens == 1 and name == 'route_rows') or (tokens > 1 and decode_only):
+                assert rc == _lib.LM_EINVAL, (tokens, name)
+                continue
+            assert rc == _lib.LM_OK, (tokens, name)
+            assert off.value % 256 == 0 and off.value + nb.value <= total, (tokens, name)
+            spans.append((off.value, off.value + nb.value))
+        spans.sort()
+        assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:])), tokens  # disjoint
+    sizes = {}
+    for name in ('hidden', 'down', 'act_q', 'act_scales', 'slot_ids', 'slot_weights',
+                 'gate_up_acc', 'down_acc'):
+        assert lib.lm_moe_workspace_region(1, _lib.WS_REGIONS[name], ctypes.byref(off),
+                                           ctypes.byref(nb)) == _lib.LM_OK
+        sizes[name] = nb.value
+    assert sizes == {'hidden': 9 * 512 * 2, 'down': 9 * 2048 * 2, 'act_q': 2048,
+                     'act_scales': 16 * 4, 'slot_ids': 32, 'slot_weights': 32,
+                     'gate_up_acc': 8 * 1024 * 4, 'down_acc': 8 * 2048 * 4}
+    assert lib.lm_moe_workspace_region(1, 13, ctypes.byref(off), ctypes.byref(nb)) == _lib.LM_EINVAL
 
 
 def test_status_maps_to_reference_exceptions():

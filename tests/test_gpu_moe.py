@@ -218,6 +218,79 @@ def test_skewed_router_bias(dev):
         assert_close(npf(out1), ref1, BF16_TOL, 'skewed decode layer')
 
 
+def test_zipf_chunk_2048(dev):
+    """One layer on the survey's skewed prefill workload at its stated size:
+    a 2048-token chunk (x ~ N(0, 1) from the device generator, seed 3) with
+    the Zipf(1.1) router bias, so the hottest expert takes about 2,000 rows
+    (21+ tiles of 96) while about 150 experts get none.  Routing ids equal
+    the oracle router's on the same normalized rows bit for bit; the layer
+    output matches the oracle on a sample of tokens that includes every
+    token routed into the hot expert's last tile, tokens from its other
+    tiles and random tokens; a HIP-graph replay equals the eager run."""
+    st = SyntheticMoEStack(layers=1, seed=3, device=dev, max_tokens=2048,
+                           router_bias=zipf_bias())
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    x = torch.randn((2048, 2048), generator=gen, device=dev).to(torch.bfloat16)
+    out, ids, _ = run_layer(st, x)
+    torch.cuda.synchronize()
+    idn = ids.cpu().numpy()
+    xn = st.workspace_view('normed', 2048).clone()
+    rows = st.workspace_view('route_rows', 2048).cpu().numpy()
+    assert np.array_equal(npf(xn), O.rmsnorm(npf(x), None, EPS))
+    _, _, ri = O.router(npf(xn), st.layer_host(0, experts=[])['router_w'], 8,
+                        st.router_bias.cpu().numpy())
+    assert np.array_equal(idn, ri)
+    counts = np.bincount(idn.reshape(-1), minlength=256)
+    hot = int(counts.argmax())
+    assert counts[hot] > 20 * 96 and (counts == 0).sum() > 120
+    # the hot expert's rows are [off, off + count) of the expert-sorted order
+    off = int(counts[:hot].sum())
+    tok_hot, slot_hot = np.nonzero(idn == hot)
+    r_hot = rows[tok_hot, slot_hot]
+    assert np.array_equal(np.sort(r_hot), np.arange(off, off + counts[hot]))
+    last_tile = off + 96 * ((counts[hot] - 1) // 96)
+    in_last = tok_hot[r_hot >= last_tile]
+    rng = np.random.default_rng(4)
+    sample = np.unique(np.concatenate([
+        in_last, rng.choice(tok_hot[r_hot < last_tile], 8, replace=False),
+        rng.choice(2048, 8, replace=False)]))
+    ref, (_, _, rs) = oracle_layer(st, npf(x)[sample], 0, idn[sample])
+    assert np.array_equal(rs, idn[sample])
+    assert_close(npf(out)[sample], ref, BF16_TOL, 'Zipf chunk sample')
+    # graph replay of the same chunk, with eager work between replays
+    static = x.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st.layer_forward(static, 0)
+    for i in range(2):
+        static.copy_(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        run_layer(st, inputs(300, 60 + i, dev))
+        torch.cuda.synchronize()
+        assert torch.equal(static, out), f'replay {i}'
+
+
+def test_tile_copy_stale_weights_refused(dev):
+    """Writing gu_q or dn_q in place after build_prefill_tiles leaves the
+    prefill tile copies stale: the stack refuses to run until they are
+    rebuilt, then runs the new weights in both prefill and decode."""
+    st = SyntheticMoEStack(layers=1, seed=17, device=dev, max_tokens=64)
+    h = inputs(16, 18, dev)
+    before, _, _ = run_layer(st, h)
+    st.dn_q[0, :, :, :8].neg_()
+    with pytest.raises(RuntimeError, match='build_prefill_tiles'):
+        run_layer(st, h)
+    with pytest.raises(RuntimeError, match='build_prefill_tiles'):
+        st.layer_forward_static(h.clone(), 0)
+    st.build_prefill_tiles()
+    after, ids, _ = run_layer(st, h)
+    assert not torch.equal(after, before)
+    ref, _ = oracle_layer(st, npf(h), 0, ids.cpu().numpy())
+    assert_close(npf(after), ref, BF16_TOL, 'rebuilt tiles')
+
+
 def _bf16_up(v):
     """The next bf16 value above each element of the bf16 tensor v (finite, nonzero)."""
     bits = v.view(torch.int16).to(torch.int32)

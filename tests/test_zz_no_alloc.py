@@ -6,7 +6,10 @@ which keeps the previous call's contents: two calls in a row with the second
 on fewer tokens (128 then 37 prefill tokens, then one decode token) must
 each equal the workspace path bit for bit - output rows, routing ids and
 routing weights - and a call beyond the array's token limit is refused before
-anything is launched.
+anything is launched.  Static calls allocate nothing (device free memory and
+torch's allocator unchanged) and can be captured in a HIP graph once the
+array is resolved (lm_moe_static_init, which the stack's wrapper calls on
+first use, outside any capture).
 """
 import pytest
 import torch
@@ -47,3 +50,44 @@ def test_static_scratch_matches_workspace_path(dev):
         st.layer_forward_static(h, 0)
     torch.cuda.synchronize()
     assert torch.equal(h, before)
+
+
+def test_static_calls_allocate_nothing_and_capture(dev):
+    """Static calls leave the device's free memory and torch's allocator
+    untouched, and captured in a HIP graph (37 prefill tokens through both
+    layers, then one decode token) every replay equals the eager calls, with
+    other static calls between the replays."""
+    st = SyntheticMoEStack(layers=2, seed=62, device=dev, max_tokens=64)
+    h37, h1 = inputs(37, 90, dev), inputs(1, 91, dev)
+    ref37, ref1 = h37.clone(), h1.clone()
+    for l in range(2):
+        st.layer_forward(ref37, l)
+        st.layer_forward(ref1, l)
+    work = [h37.clone(), h1.clone(), inputs(5, 92, dev)]
+    st.layer_forward_static(inputs(3, 94, dev), 0)  # first use: resolves the array
+    torch.cuda.synchronize()
+    free0, alloc0 = torch.cuda.mem_get_info(dev)[0], torch.cuda.memory_allocated(dev)
+    for _ in range(3):
+        for x in work:
+            for l in range(2):
+                st.layer_forward_static(x, l)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info(dev)[0] == free0
+    assert torch.cuda.memory_allocated(dev) == alloc0
+    s37, s1 = h37.clone(), h1.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for l in range(2):
+            st.layer_forward_static(s37, l)
+        for l in range(2):
+            st.layer_forward_static(s1, l)
+    for i in range(3):
+        s37.copy_(h37)
+        s1.copy_(h1)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(s37, ref37), f'replay {i}: 37 tokens'
+        assert torch.equal(s1, ref1), f'replay {i}: 1 token'
+        other = inputs(9, 93 + i, dev)
+        st.layer_forward_static(other, i % 2)  # eager static work between replays
+        torch.cuda.synchronize()
