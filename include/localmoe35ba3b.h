@@ -65,11 +65,19 @@ int lm_quantize_weight_g128(const float *w, int8_t *q, float *s,
  *   tiles[e * expert_stride + ((b * k/64 + s) * 1024) + 256 p + 16 r + j]
  *     = q[e][16 b + r][64 s + 16 p + j],   r < 16, p < 4, j < 16.
  * Each 16-row x 64-K block is 1 KB, its 16-byte pieces ordered piece-major,
- * so lane 16 p + r of a wave loads exactly its MFMA operand piece.  tiles
- * has q's size and expert stride; n % 16 == 0, k % 64 == 0.  No counterpart
- * in the reference (a re-layout of convert.py's int8 format). */
+ * so lane 16 p + r of a wave loads exactly its MFMA operand piece.
+ * format LM_TILES_PLAIN stores the bytes as they are; LM_TILES_F16 stores
+ * u = q + 128 and, within every 4-byte word, the bytes of k = 0, 2, 1, 3
+ * (the form the fused layer's fp16 gate_up GEMM converts to fp16 q with one
+ * mask, one byte permute and one packed subtraction per two weights; see
+ * lm_moe_layer.gu_q_tiles).  tiles has q's size and expert stride;
+ * n % 16 == 0, k % 64 == 0.  No counterpart in the reference (a re-layout of
+ * convert.py's int8 format). */
+#define LM_TILES_PLAIN 0
+#define LM_TILES_F16 1
 int lm_w8_tile_rows(const int8_t *q, int64_t experts, int64_t n, int64_t k,
-                    int64_t expert_stride, int8_t *tiles, void *stream);
+                    int64_t expert_stride, int8_t *tiles, int format,
+                    void *stream);
 
 /* Dynamic activation quantization per row and 128-group:
  * s = max(amax, 1e-10) * (1/127), q = rint(x / s).  x [rows, k] (x_dtype).
@@ -281,11 +289,19 @@ typedef struct lm_moe_layer {
   /* Optional copies of gu_q and dn_q in the 16-row tile layout of
    * lm_w8_tile_rows (same expert strides), which the prefill grouped GEMMs
    * read with contiguous 1 KB wave loads; NULL = they read gu_q / dn_q.
-   * Results are identical either way.  No counterpart in the reference: a
-   * device-side cache of the bank (for callers that can spend the memory of
-   * a second int8 copy). */
+   * dn_q_tiles is in LM_TILES_PLAIN and leaves results bit-identical.
+   * gu_q_tiles is in the format gu_q_tiles_format names: LM_TILES_PLAIN
+   * leaves results bit-identical; with LM_TILES_F16 the prefill gate_up GEMM
+   * runs on fp16 operands - exact fp16 copies of the normalized rows (a
+   * power of two per row) times exact q - and applies each 128-group's
+   * scale to the fp32 sums instead of rounding q * s to bf16 per weight
+   * (int8.py:21): within the bf16 tolerance of the reference's arithmetic,
+   * not bit-identical to it, and faster.  No counterpart in the reference:
+   * a device-side cache of the bank (for callers that can spend the memory
+   * of a second int8 copy). */
   const int8_t *gu_q_tiles;
   const int8_t *dn_q_tiles;
+  int64_t gu_q_tiles_format; /* LM_TILES_PLAIN or LM_TILES_F16 */
 } lm_moe_layer;
 
 int64_t lm_moe_workspace_bytes(int64_t max_tokens, int64_t hidden,

@@ -14,6 +14,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / 'liblocalmoe35ba3b.so'
 
 LM_OK, LM_EINVAL, LM_ENOMEM, LM_ELAUNCH = 0, 1, 2, 3
 LM_BF16, LM_FP16, LM_FP32 = 0, 1, 2
+LM_TILES_PLAIN, LM_TILES_F16 = 0, 1
 # fused-layer workspace regions (lm_moe_workspace_region)
 WS_REGIONS = {'normed': 0, 'gate': 1, 'ids': 2, 'weights': 3, 'route_rows': 4, 'hidden': 5,
               'down': 6, 'act_q': 7, 'act_scales': 8, 'slot_ids': 9, 'slot_weights': 10,
@@ -29,7 +30,7 @@ SIGNATURES = {
     'lm_version': (ctypes.c_char_p, []),
     'lm_last_error': (ctypes.c_char_p, []),
     'lm_quantize_weight_g128': (I32, [P, P, P, I64, I64, P]),
-    'lm_w8_tile_rows': (I32, [P, I64, I64, I64, I64, P, P]),
+    'lm_w8_tile_rows': (I32, [P, I64, I64, I64, I64, P, I32, P]),
     'lm_act_quant_g128': (I32, [P, I32, P, P, I64, I64, P]),
     'lm_w8a16_linear': (I32, [P, P, P, P, I64, I64, I64, I32, I32, P]),
     'lm_w8a16_grouped_gemv': (I32, [P, P, P, I64, I64, I64, I32, I32, I32, P]),
@@ -68,7 +69,7 @@ class MoeLayer(ctypes.Structure):
                 ('gu_q', P), ('gu_s', P), ('dn_q', P), ('dn_s', P),
                 ('gu_q_expert_stride', I64), ('gu_s_expert_stride', I64),
                 ('dn_q_expert_stride', I64), ('dn_s_expert_stride', I64),
-                ('gu_q_tiles', P), ('dn_q_tiles', P)]
+                ('gu_q_tiles', P), ('dn_q_tiles', P), ('gu_q_tiles_format', I64)]
 
     def __init__(self, *args, **kw):
         super().__init__(ctypes.sizeof(MoeLayer), *args, **kw)

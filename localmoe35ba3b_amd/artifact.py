@@ -23,6 +23,7 @@ import pathlib
 import torch
 from safetensors.torch import load_file
 
+from . import _lib
 from .convert import quantize_g128
 
 FORMAT = 'q36-w8a16-g128-rtn-fp32scale-v1'
@@ -107,7 +108,7 @@ class Artifact:
 
 
 def stack_from_artifact(root, device='cuda', layers=None, max_tokens=2048, verify=True,
-                        prefill_tiles=True):
+                        prefill_tiles=True, gate_up_format=_lib.LM_TILES_F16):
     """MoEStack of the fused layer path filled from a converted checkpoint.
 
     Per layer l: routed experts from mlp.experts.{gate_up_proj, down_proj};
@@ -115,7 +116,8 @@ def stack_from_artifact(root, device='cuda', layers=None, max_tokens=2048, verif
     (rows concatenated) and .down_proj; router = mlp.gate.weight (bf16),
     shared gate = mlp.shared_expert_gate.weight, RMSNorm weight =
     post_attention_layernorm.weight.  With prefill_tiles the prefill GEMMs
-    read a tile-layout copy of the int8 bank (MoEStack.build_prefill_tiles).
+    read a tile-layout copy of the int8 bank, gate_up's in `gate_up_format`
+    (MoEStack.build_prefill_tiles).
     """
     from .runtime.stack import MoEStack
     art = Artifact(root, verify=verify)
@@ -149,5 +151,5 @@ def stack_from_artifact(root, device='cuda', layers=None, max_tokens=2048, verif
         st.norm_w[l].copy_(art.load(p + '.post_attention_layernorm.weight', dev)['weight']
                            .reshape(-1).float())
     if prefill_tiles:
-        st.build_prefill_tiles()
+        st.build_prefill_tiles(gate_up_format)
     return st

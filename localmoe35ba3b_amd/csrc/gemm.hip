@@ -44,7 +44,8 @@ struct GemmArgs {
   int64_t x_rows;
   const int8_t *q;
   int64_t q_es;
-  const int8_t *q_tiles;  // q in the 16-row tile layout (weight load mode kWlTiles)
+  const int8_t *q_tiles;  // q in the 16-row tile layout (weight load modes kWlTiles*)
+  const int *x_exp;       // kWlTilesF16: x row r holds fp16(x_r * 2^x_exp[r]) exactly
   const float *s;
   int64_t s_es;
   uint16_t *y;
@@ -271,6 +272,24 @@ __device__ __forceinline__ u32x4 dequant8s(uint2 w, float s) {
                T::pack2(f[6], f[7])};
 }
 
+// Eight weights of the LM_TILES_F16 format (bytes u = q + 128, each dword
+// holding k = 0, 2, 1, 3 in byte order) -> eight fp16 values q, exactly, in k
+// order.  A byte placed under the fp16 exponent of 1024 is the value 1024 + u
+// (one v_bitop3 (S0 & S1) | S2 for k = 0, 1, one byte permute for k = 2, 3);
+// subtracting 1152 leaves q.  Four VALU operations per four weights, against
+// eleven for the exact bf16(q * s).
+__device__ __forceinline__ u32x4 dequant8_f16(uint2 w) {
+  constexpr unsigned kAndOr = (0xF0u & 0xCCu) | 0xAAu;  // bitop3 table of (S0 & S1) | S2
+  const f16x2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  auto sub = [&](uint32_t m) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, m) + bias);
+  };
+  return u32x4{sub(__builtin_amdgcn_bitop3_b32(w.x, 0x00FF00FFu, 0x64006400u, kAndOr)),
+               sub(__builtin_amdgcn_perm(0x64646464u, w.x, 0x07030701u)),
+               sub(__builtin_amdgcn_bitop3_b32(w.y, 0x00FF00FFu, 0x64006400u, kAndOr)),
+               sub(__builtin_amdgcn_perm(0x64646464u, w.y, 0x07030701u))};
+}
+
 // SiLU for the prefill epilogue from the hardware exp2 and reciprocal
 // (about 2 ulp in fp32); the product is rounded to bf16 right after.
 __device__ __forceinline__ float silu_fast(float x) {
@@ -490,7 +509,20 @@ __device__ __forceinline__ void barrier_raw() { asm volatile("s_barrier" ::: "me
 //   kWlTiles   streamed weights in the 16-row tile layout (lm_w8_tile_rows):
 //              a wave's load of one 16-row x 64-K block is 1 KB contiguous
 //              and lands in the MFMA layout, no permute.
-constexpr int kWlDirect = 0, kWlPermute = 1, kWlTiles = 2;
+//   kWlTilesF16  the tile layout in its fp16 format (LM_TILES_F16) on fp16
+//              activation rows x_r = fp16(row r * 2^x_exp[r]) (exact): the
+//              MFMAs multiply exact fp16 q by the exact rows in fp16 with
+//              fp32 accumulation, and the group scales act on the
+//              accumulators.  Before the first MFMA of group g each
+//              accumulator of column n is multiplied by s[n, g-1] / s[n, g],
+//              so it always holds sum_{g' <= g} s[n, g'] P_g' / s[n, g]; the
+//              epilogue multiplies by s[n, G-1] and 2^-x_exp[r].  The
+//              accumulator of a tile was last written 16 MFMAs earlier, so
+//              the multiply waits for nothing.  Scales are clamped into
+//              [2^-40, 2^40] for the ratios (a clamped group contributes at
+//              most 2^-40 |P| instead of nothing).  Unlike the bf16 path this
+//              does not round q * s to bf16 before the products.
+constexpr int kWlDirect = 0, kWlPermute = 1, kWlTiles = 2, kWlTilesF16 = 3;
 //
 // A stage in LDS: BM rows x 128 B (64 bf16); 16-byte chunk p of row r is
 // stored at chunk p ^ rb_swz(r).  Scales of the tile are staged once,
@@ -530,9 +562,20 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   constexpr int A_W = (MS * 16 / RPL + NW - 1) / NW;  // wave-loads per wave covering 16 MS rows
   constexpr int SC_P = BN * G / 4;            // 16-byte scale pieces of the tile
   constexpr int SC_W = (SC_P + NT - 1) / NT;
-  constexpr int U = BD / rb_gcd(BD, AS) * AS;   // unroll: both ring indices static
+  constexpr int U0 = BD / rb_gcd(BD, AS) * AS;  // unroll: both ring indices static
+  constexpr int GS = 128 / KS;                   // stages per scale group
+  // kWlTilesF16 also needs the group boundaries static in the unrolled loop
+  constexpr int U = WL == kWlTilesF16 && U0 % GS ? U0 * GS / rb_gcd(U0, GS) : U0;
   static_assert(MS * 16 <= BM && BD >= 2 && AD >= 2 && NW * A_W * RPL <= BM, "shape");
-  float *scl = reinterpret_cast<float *>(smem + AR * A_STAGE);  // [G][BN]
+  constexpr bool F16 = WL == kWlTilesF16;
+  constexpr bool TILES = WL == kWlTiles || F16;
+  using MT = typename std::conditional<F16, FP16, T>::type;  // MFMA operand type
+  static_assert(!F16 || G % 4 == 0, "fp16 tiles: whole 16-byte scale pieces per column");
+  // [G][BN] fp32 scales, or (kWlTilesF16) the ratios s[g-1] / s[g] (1 at
+  // g = 0); then (kWlTilesF16) s[G-1] per column and the x_exp of each row
+  float *scl = reinterpret_cast<float *>(smem + AR * A_STAGE);
+  float *slast = scl + G * BN;
+  int *rowk = reinterpret_cast<int *>(slast + BN);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -579,7 +622,7 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   const int8_t *bsrc[NI];
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    if constexpr (WL == kWlTiles) {
+    if constexpr (TILES) {
       const int wr = wrow(col_base(ni));
       bsrc[ni] = a.q_tiles + e * a.q_es + (int64_t)((wr >= 0 ? wr : 0) >> 4) * (K / 64) * 1024 +
                  lane * 16;
@@ -599,6 +642,13 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
     const int rr = min(r, rows - 1);
     const int64_t xr = GATHER ? clamp_index(a.pos[start + rr], a.x_rows) : start + rr;
     asrc[j] = a.x + xr * a.ldx + (((lane % CPR) ^ rb_swz(r)) * 8);
+  }
+  // kWlTilesF16: thread t < BM fetches the exponent of tile row t (consumed
+  // in the epilogue; written to LDS before the last stage's barrier)
+  int rk = 0;
+  if constexpr (F16) {
+    const int rr = min(tid, rows - 1);
+    rk = a.x_exp[GATHER ? clamp_index(a.pos[start + rr], a.x_rows) : start + rr];
   }
 
   u32x4 breg[BD][NI][HL];
@@ -624,13 +674,13 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   // leaves the caches to the activation rows and the next kernel's inputs.
   // Fuller tiles (the shared expert's, a hot expert's) keep cached loads, as
   // other row tiles of the same expert re-read their weights.
-  constexpr bool NTW = WL == kWlTiles && MS < 6;
+  constexpr bool NTW = TILES && MS < 6;
   auto load_b = [&](int slot, int s) {
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
       for (int h = 0; h < HL; ++h) {
-        const int8_t *p = bsrc[ni] + (WL == kWlTiles ? (s * HL + h) * 1024 : s * KS + 64 * h);
+        const int8_t *p = bsrc[ni] + (TILES ? (s * HL + h) * 1024 : s * KS + 64 * h);
         breg[slot][ni][h] = NTW ? ldg16_nt(p) : ldg16(p);
       }
   };
@@ -666,9 +716,25 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   for (int j = 0; j < SC_W; ++j) {
     const int piece = tid + NT * j;
     const int c = piece / (G / 4), g0 = 4 * (piece % (G / 4));
-    if (piece < SC_P) {
+    if constexpr (F16) {
+      // the column's pieces sit in consecutive lanes: group g0 - 1 is the
+      // last of the previous lane's four
+      float sc[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) scl[(g0 + i) * BN + c] = __uint_as_float(sreg[j][i]);
+      for (int i = 0; i < 4; ++i)
+        sc[i] = fminf(fmaxf(__uint_as_float(sreg[j][i]), 0x1.0p-40f), 0x1.0p40f);
+      const float prev = __shfl_up(sc[3], 1, 64);
+      if (piece < SC_P) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          scl[(g0 + i) * BN + c] = g0 + i == 0 ? 1.0f : (i ? sc[i - 1] : prev) / sc[i];
+        if (g0 + 4 == G) slast[c] = sc[3];
+      }
+    } else {
+      if (piece < SC_P) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) scl[(g0 + i) * BN + c] = __uint_as_float(sreg[j][i]);
+      }
     }
   }
 #pragma unroll
@@ -682,9 +748,11 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
     const int g = (s * KS) >> 7;
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
-      const float sc = scl[g * BN + col_base(ni) + (lane & 15)];
-      out[ni] = dequant8s<T>(
-          uint2{breg[ub][ni][p >> 1][2 * (p & 1)], breg[ub][ni][p >> 1][2 * (p & 1) + 1]}, sc);
+      const uint2 w{breg[ub][ni][p >> 1][2 * (p & 1)], breg[ub][ni][p >> 1][2 * (p & 1) + 1]};
+      if constexpr (F16)
+        out[ni] = dequant8_f16(w);
+      else
+        out[ni] = dequant8s<T>(w, scl[g * BN + col_base(ni) + (lane & 15)]);
     }
   };
   // The B operand of the piece being multiplied; the next piece (the first
@@ -695,8 +763,19 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   barrier_raw();
   rb_perm(0);
   dq(0, 0, 0, bcur);
-  auto step = [&](int s, int ub, int ua, bool st_a, bool ld_a, bool ld_b, bool has_next) {
+  // resc: stage s opens a scale group (kWlTilesF16 rescales the accumulators)
+  auto step = [&](int s, int ub, int ua, bool st_a, bool ld_a, bool ld_b, bool has_next,
+                  bool resc) {
+    float rr[NI];
+    if constexpr (F16) {
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        rr[ni] = resc ? scl[((s * KS) >> 7) * BN + col_base(ni) + (lane & 15)] : 1.0f;
+    }
     if (st_a) store_a(ua, s + 1);
+    if constexpr (F16) {
+      if (!has_next && tid < BM) rowk[tid] = rk;  // read by the epilogue, after this barrier
+    }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
     barrier_raw();
     if (ld_a) load_a(ua, s + AD);
@@ -724,8 +803,10 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
 #pragma unroll
       for (int mi = 0; mi < MS; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < NI; ++ni)
-          acc[mi][ni] = T::mfma16x16x32(af[mi], bcur[ni], acc[mi][ni]);
+        for (int ni = 0; ni < NI; ++ni) {
+          if (F16 && resc && p == 0) acc[mi][ni] = acc[mi][ni] * rr[ni];
+          acc[mi][ni] = MT::mfma16x16x32(af[mi], bcur[ni], acc[mi][ni]);
+        }
       __builtin_amdgcn_sched_barrier(0);
       if (nxt) {
 #pragma unroll
@@ -741,12 +822,14 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   static_assert(TL <= KT, "stage count");
   for (int s0 = 0; s0 < KT - TL; s0 += U) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) step(s0 + u, u % BD, (u + 1) % AS, true, true, true, true);
+    for (int u = 0; u < U; ++u)
+      step(s0 + u, u % BD, (u + 1) % AS, true, true, true, true, (u * KS) % 128 == 0);
   }
 #pragma unroll
   for (int v = 0; v < TL; ++v) {
     const int s = KT - TL + v;
-    step(s, s % BD, (s + 1) % AS, s + 1 < KT, s + AD < KT, s + BD - 1 < KT, s + 1 < KT);
+    step(s, s % BD, (s + 1) % AS, s + 1 < KT, s + AD < KT, s + BD - 1 < KT, s + 1 < KT,
+         (s * KS) % 128 == 0);
   }
 
 #pragma unroll
@@ -756,13 +839,19 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
       const int rl = mi * 16 + q * 4 + it;
       if (rl >= rows) continue;
       uint16_t *yrow = a.y + (start + rl) * a.ldy;
+      // kWlTilesF16: the last group's scale, then the row's power of two (exact)
+      const int kr = F16 ? rowk[rl] : 0;
+      auto val = [&](int ni) {
+        return F16 ? ldexpf(acc[mi][ni][it] * slast[col_base(ni) + (lane & 15)], -kr)
+                   : acc[mi][ni][it];
+      };
       if constexpr (SWIGLU) {
 #pragma unroll
         for (int ni = 0; ni < NI / 2; ++ni) {
           const int col = n0 + wave * (TN / 2) + ni * 16 + (lane & 15);
           if (col < half) {
-            const float gate = T::round(acc[mi][ni][it]);
-            const float up = T::round(acc[mi][ni + NI / 2][it]);
+            const float gate = T::round(val(ni));
+            const float up = T::round(val(ni + NI / 2));
             yrow[col] = T::from_f32(T::round(silu_fast(gate)) * up);
           }
         }
@@ -770,7 +859,7 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
           const int col = n0 + col_base(ni) + (lane & 15);
-          if (col < a.N) yrow[col] = T::from_f32(acc[mi][ni][it]);
+          if (col < a.N) yrow[col] = T::from_f32(val(ni));
         }
       }
     }
@@ -780,7 +869,7 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
 template <typename T, bool SWIGLU, bool GATHER, int WL, int K, int BM, int TN, int BD, int HL,
           int AD, int NW, int OCC>
 __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
-  constexpr int SC_BYTES = NW * TN * (K / 128) * 4;
+  constexpr int SC_BYTES = NW * TN * (K / 128) * 4 + (WL == kWlTilesF16 ? (NW * TN + BM) * 4 : 0);
   __shared__ __align__(16) unsigned char smem[3 * BM * 128 * HL + SC_BYTES];
   int mt, nt;
   if (!xcd_tile(a, mt, nt)) return;
@@ -830,8 +919,9 @@ constexpr int kGroupedBN = 128;  // grouped_mfma_kernel tile columns
 
 template <typename T, bool SWIGLU, bool GATHER, int WL, int K>
 static int launch_rb(GemmArgs a, unsigned mtiles, hipStream_t st) {
-  constexpr int TN = WL == kWlTiles ? kRbTnTiles : kRbTN;
-  constexpr int OCC = WL == kWlTiles ? kRbOccTiles : kRbOcc;
+  constexpr bool TILES = WL == kWlTiles || WL == kWlTilesF16;
+  constexpr int TN = TILES ? kRbTnTiles : kRbTN;
+  constexpr int OCC = TILES ? kRbOccTiles : kRbOcc;
   constexpr int RBN = kRbNW * TN;
   a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, RBN / 2) : (int)cdiv(a.N, RBN);
   a.mt_count = (int)mtiles;
@@ -903,6 +993,12 @@ static int routed_dispatch(const GemmArgs &a, unsigned mt, bool gather, bool swi
   // The tile layout serves the fused layer's two GEMMs (gathered gate_up +
   // SwiGLU, contiguous down) in bf16; every other form reads q.
   const bool tiles = a.q_tiles != nullptr && std::is_same<T, BF16>::value;
+  if (a.x_exp) {  // fp16 rows on LM_TILES_F16 weights, bf16 out (checked by routed_gemm)
+    if constexpr (std::is_same<T, BF16>::value) {
+      if (swiglu && gather) return launch_grouped<T, true, true, kWlTilesF16>(a, mt, st);
+    }
+    return set_error(LM_EINVAL, "fp16 tiles serve the gathered gate_up GEMM with SwiGLU");
+  }
   if (swiglu) {
     if (gather)
       return tiles ? launch_grouped<T, true, true, kWlTiles>(a, mt, st)
@@ -927,12 +1023,17 @@ int routed_gemm(const RoutedGemm &r, hipStream_t st) {
   a.q = r.q;
   a.q_es = r.q_es;
   a.q_tiles = r.q_tiles;
+  a.x_exp = r.x_exp;
   a.s = r.s;
   a.s_es = r.s_es;
   a.y = static_cast<uint16_t *>(r.y);
   a.ldy = r.swiglu ? r.n / 2 : r.n;
   LM_REQUIRE(!r.q_tiles || (r.n % 32 == 0 && r.k % 64 == 0), LM_EINVAL,
              "the tile layout needs n % 32 == 0 and k % 64 == 0");
+  LM_REQUIRE(!r.x_exp || (r.q_tiles && r.dtype == LM_BF16 && r.bm <= 96 &&
+                          (r.k == 2048 || r.k == 512)),
+             LM_EINVAL, "fp16 rows need LM_TILES_F16 weights, bf16 output, tiles <= 96 rows "
+                        "and k = 2048 or 512");
   a.N = (int)r.n;
   a.K = (int)r.k;
   a.tile_rows = (int)r.bm;

@@ -31,6 +31,9 @@ struct RoutedGemm {
   bool gather, swiglu;
   int dtype;
   const int8_t *q_tiles = nullptr;  // q in the lm_w8_tile_rows layout, or null
+  // Non-null: x holds fp16 rows fp16(row r * 2^x_exp[r]) (exact) and q_tiles
+  // is in the LM_TILES_F16 format; the output is bf16.
+  const int *x_exp = nullptr;
 };
 int routed_gemm(const RoutedGemm &r, hipStream_t st);
 

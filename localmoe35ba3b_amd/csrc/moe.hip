@@ -35,8 +35,8 @@ constexpr int kTopkTokens = 8;  // prefill top-k: tokens (waves) per workgroup
 static_assert(kE == 256, "the prefill kernels map one thread of a 256-thread workgroup to each expert");
 
 struct WsLayout {
-  int64_t bcounts, xn, gl, logits, nx, nw, ids, wts, sel, selw, xq, xs, dacc_gu, dacc_dn, pos,
-      table, rslot, rpos, hbuf, vbuf, total;
+  int64_t bcounts, xn, xh, xk, gl, logits, nx, nw, ids, wts, sel, selw, xq, xs, dacc_gu, dacc_dn,
+      pos, table, rslot, rpos, hbuf, vbuf, total;
   int64_t max_tiles, n_tiles;
 };
 
@@ -54,6 +54,8 @@ constexpr WsLayout layout(int64_t T) {
     return at;
   };
   w.xn = take(T * kH * 2);
+  w.xh = take(T * kH * 2);  // prefill: fp16(xn * 2^xk) for the fp16 gate_up GEMM
+  w.xk = take(T * 4);       // prefill: the per-row power of two of xh
   w.gl = take(T * 4);
   w.logits = take(T * kE * 4);
   w.nx = take(T * 4);
@@ -91,6 +93,8 @@ struct LayerArgs {
   float eps;
   // workspace views
   uint16_t *xn;
+  uint16_t *xh;  // prefill: fp16(xn * 2^xk), exact
+  int *xk;
   float *gl;
   float *logits;
   float *nx;  // prefill: |xn| of each token row
@@ -645,6 +649,7 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, c
   __shared__ float xf[kH];
   __shared__ float red[4];
   __shared__ float red2[4];
+  __shared__ float redm[4];
   __shared__ double dred[4];
   const int tok = blockIdx.x;
   const int t = threadIdx.x;
@@ -674,12 +679,21 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, c
     return;
   }
   norm_row_to_lds(ldg16(a.h + (int64_t)tok * kH + t * PER), nwv, a.eps, xf, red);
+  float am = 0.0f;
   {
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) ss += xf[t * PER + j] * xf[t * PER + j];
+    for (int j = 0; j < PER; ++j) {
+      ss += xf[t * PER + j] * xf[t * PER + j];
+      am = fmaxf(am, fabsf(xf[t * PER + j]));
+    }
     ss = wave_sum_f32(ss);
-    if ((t & 63) == 0) red2[t >> 6] = ss;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+    if ((t & 63) == 0) {
+      red2[t >> 6] = ss;
+      redm[t >> 6] = am;
+    }
   }
   u32x4 packed;
 #pragma unroll
@@ -698,6 +712,26 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, c
   if (t == 0) {
     a.gl[tok] = round_bf16((float)(dred[0] + dred[1] + dred[2] + dred[3]));
     a.nx[tok] = sqrtf((red2[0] + red2[1]) + (red2[2] + red2[3]));
+  }
+  // The fp16 copy of the row for the gate_up GEMM: xn * 2^k with the row's
+  // largest |value| in [2^14, 2^15).  A bf16 value with |v| 2^k >= 2^-17 is
+  // exact in fp16; smaller ones (below 2^-31 of the row maximum) round to the
+  // fp16 subnormal grid.
+  {
+    int ex = 0;
+    const float m = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
+    (void)frexpf(m, &ex);
+    const int k = m > 0.0f ? min(max(15 - ex, -126), 126) : 0;
+    u32x4 hp;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f16x2 v;
+      v.x = (_Float16)ldexpf(xf[t * PER + 2 * j], k);
+      v.y = (_Float16)ldexpf(xf[t * PER + 2 * j + 1], k);
+      hp[j] = __builtin_bit_cast(uint32_t, v);
+    }
+    *reinterpret_cast<u32x4 *>(a.xh + (int64_t)tok * kH + t * PER) = hp;
+    if (t == 0) a.xk[tok] = k;
   }
   if (tok < kE) router_row_norm();
 }
@@ -1322,6 +1356,9 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   LM_REQUIRE(layer->router_w && layer->shared_gate_w && layer->gu_q && layer->gu_s &&
                  layer->dn_q && layer->dn_s,
              LM_EINVAL, "null layer weight");
+  LM_REQUIRE(layer->gu_q_tiles_format == LM_TILES_PLAIN ||
+                 layer->gu_q_tiles_format == LM_TILES_F16,
+             LM_EINVAL, "unknown gu_q_tiles_format");
   const WsLayout w = layout(tokens);
   LM_REQUIRE(workspace_bytes >= w.total, LM_ENOMEM, "workspace too small for this token count");
   unsigned char *ws = static_cast<unsigned char *>(workspace);
@@ -1341,6 +1378,8 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   a.h = static_cast<uint16_t *>(h);
   a.eps = eps;
   a.xn = reinterpret_cast<uint16_t *>(ws + w.xn);
+  a.xh = reinterpret_cast<uint16_t *>(ws + w.xh);
+  a.xk = reinterpret_cast<int *>(ws + w.xk);
   a.gl = reinterpret_cast<float *>(ws + w.gl);
   a.logits = reinterpret_cast<float *>(ws + w.logits);
   a.nx = reinterpret_cast<float *>(ws + w.nx);
@@ -1409,9 +1448,13 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   // gate_up over the T token rows gathered through pos, down over the R + T
   // rows of hbuf; the banks hold E + 1 experts (index E = shared expert)
   // (the weights' tile-layout copies, when the caller provides them)
-  const RoutedGemm gu{a.xn,    kH,      T,  a.gu_q, a.gu_s,  a.gu_qes, a.gu_ses,
+  // With an LM_TILES_F16 copy of gu_q the GEMM runs in fp16 on xh (exact
+  // copies of the normalized rows); otherwise in bf16 on xn.
+  const bool f16 = layer->gu_q_tiles != nullptr && layer->gu_q_tiles_format == LM_TILES_F16;
+  const RoutedGemm gu{f16 ? a.xh : a.xn, kH,  T,  a.gu_q, a.gu_s,  a.gu_qes, a.gu_ses,
                       kE + 1,  pos,     table, w.n_tiles, kBM, a.hbuf, R + T,
-                      2 * kI,  kH,      true,  true,   LM_BF16, layer->gu_q_tiles};
+                      2 * kI,  kH,      true,  true,   LM_BF16, layer->gu_q_tiles,
+                      f16 ? a.xk : nullptr};
   if (int rc = routed_gemm(gu, st)) return rc;
   if (int rc = mark(5)) return rc;
   const RoutedGemm dn{a.hbuf,  kI,      R + T, a.dn_q, a.dn_s, a.dn_qes, a.dn_ses,

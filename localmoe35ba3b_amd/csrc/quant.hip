@@ -102,31 +102,43 @@ extern "C" int lm_quantize_weight_g128(const float *w, int8_t *q, float *s, int6
 
 // The 16-row tile layout of an int8 bank (lm_w8_tile_rows): one wave per
 // 1 KB block (16 rows x 64 K of one expert); lane 16 p + r copies piece p
-// (16 bytes) of row r to byte 16 (16 p + r) of the block.
+// (16 bytes) of row r to byte 16 (16 p + r) of the block.  The fp16 format
+// (LM_TILES_F16) also biases each byte to u = q + 128 and stores the bytes of
+// every dword in the order k = 0, 2, 1, 3, which the GEMM's fp16 conversion
+// takes apart with one mask and one byte permute.
 __global__ __launch_bounds__(256) void tile_rows_kernel(const int8_t *__restrict__ q,
                                                         int8_t *__restrict__ tiles, int64_t blocks,
                                                         int64_t nb, int64_t kb, int64_t k,
-                                                        int64_t es) {
+                                                        int64_t es, int fmt) {
   const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (blk >= blocks) return;
   const int lane = threadIdx.x & 63, p = lane >> 4, r = lane & 15;
   const int64_t e = blk / (nb * kb), rem = blk - e * nb * kb;
   const int64_t b = rem / kb, s = rem - b * kb;
-  const u32x4 v = ldg16(q + e * es + (16 * b + r) * k + 64 * s + 16 * p);
+  u32x4 v = ldg16(q + e * es + (16 * b + r) * k + 64 * s + 16 * p);
+  if (fmt == LM_TILES_F16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t u = v[i] ^ 0x80808080u;
+      v[i] = (u & 0xFF0000FFu) | ((u >> 8) & 0x0000FF00u) | ((u << 8) & 0x00FF0000u);
+    }
+  }
   *reinterpret_cast<u32x4 *>(tiles + e * es + (b * kb + s) * 1024 + lane * 16) = v;
 }
 
 extern "C" int lm_w8_tile_rows(const int8_t *q, int64_t experts, int64_t n, int64_t k,
-                               int64_t expert_stride, int8_t *tiles, void *stream) {
+                               int64_t expert_stride, int8_t *tiles, int format, void *stream) {
   LM_REQUIRE(experts >= 0 && n > 0 && k > 0 && n % 16 == 0 && k % 64 == 0, LM_EINVAL,
              "the tile layout needs n % 16 == 0 and k % 64 == 0");
   LM_REQUIRE(expert_stride >= n * k, LM_EINVAL, "expert stride smaller than n * k");
+  LM_REQUIRE(format == LM_TILES_PLAIN || format == LM_TILES_F16, LM_EINVAL,
+             "unknown tile format");
   LM_REQUIRE(experts == 0 || (q && tiles), LM_EINVAL, "null pointer");
   const int64_t nb = n / 16, kb = k / 64, blocks = experts * nb * kb;
   if (blocks == 0) return LM_OK;
   LM_REQUIRE((blocks + 3) / 4 < (int64_t(1) << 31), LM_EINVAL, "bank too large for one launch");
   tile_rows_kernel<<<(unsigned)((blocks + 3) / 4), 256, 0, as_stream(stream)>>>(
-      q, tiles, blocks, nb, kb, k, expert_stride);
+      q, tiles, blocks, nb, kb, k, expert_stride, format);
   return check_launch("tile_rows_kernel");
 }
 

@@ -104,22 +104,28 @@ class MoEStack:
             return 0
         return (self.gu_q_tiles.numel() + self.dn_q_tiles.numel()) * self.gu_q_tiles.element_size()
 
-    def build_prefill_tiles(self):
+    def build_prefill_tiles(self, gate_up_format=_lib.LM_TILES_F16):
         """Copies of gu_q and dn_q in the 16-row tile layout (lm_w8_tile_rows)
         for the prefill grouped GEMMs, which then read each 16-row x 64-K
-        weight block as one contiguous 1 KB wave load.  Costs a second int8
-        bank in HBM (about 32 GB for 40 layers); results are identical with
-        or without.  Call again after changing gu_q / dn_q."""
+        weight block as one contiguous 1 KB wave load.  gu_q's copy is in
+        `gate_up_format`: LM_TILES_F16 (default) runs the gate_up GEMM on
+        fp16 operands with the group scales applied to the fp32 sums (within
+        the bf16 tolerance of the reference's arithmetic, faster);
+        LM_TILES_PLAIN keeps the exact bf16(q * s) dequantization, bit for
+        bit.  dn_q's copy is plain.  Costs a second int8 bank in HBM (about
+        32 GB for 40 layers).  Call again after changing gu_q / dn_q."""
         if self.gu_q_tiles is None:
             self.gu_q_tiles = torch.empty_like(self.gu_q)
             self.dn_q_tiles = torch.empty_like(self.dn_q)
         st = _lib.stream(self.device)
         for l in range(self.L):
-            for q, t in ((self.gu_q, self.gu_q_tiles), (self.dn_q, self.dn_q_tiles)):
+            for q, t, fmt in ((self.gu_q, self.gu_q_tiles, gate_up_format),
+                              (self.dn_q, self.dn_q_tiles, _lib.LM_TILES_PLAIN)):
                 _lib.call('lm_w8_tile_rows', q[l].data_ptr(), q.shape[1], q.shape[2], q.shape[3],
-                          q.stride(1), t[l].data_ptr(), st)
+                          q.stride(1), t[l].data_ptr(), fmt, st)
             self._structs[l].gu_q_tiles = self.gu_q_tiles[l].data_ptr()
             self._structs[l].dn_q_tiles = self.dn_q_tiles[l].data_ptr()
+            self._structs[l].gu_q_tiles_format = gate_up_format
         self._tiles_of = self._bank_versions()
         return self
 
@@ -312,11 +318,11 @@ class SyntheticMoEStack(MoEStack):
     """Random-init 35B-A3B-class MoE-FFN stack resident in HBM: weights drawn
     on the GPU from per-(layer, matrix) seeds, N(0, 0.02) fp32, quantized by
     the group-128 HIP quantizer; RMSNorm weight zero.  With prefill_tiles the
-    prefill GEMMs read a tile-layout copy of the int8 bank
-    (build_prefill_tiles)."""
+    prefill GEMMs read a tile-layout copy of the int8 bank, gate_up's in
+    `gate_up_format` (build_prefill_tiles)."""
 
     def __init__(self, layers=40, seed=4, device='cuda', max_tokens=2048, router_bias=None,
-                 chunk_experts=32, prefill_tiles=True):
+                 chunk_experts=32, prefill_tiles=True, gate_up_format=_lib.LM_TILES_F16):
         super().__init__(layers, device, max_tokens, router_bias)
         dev = self.device
         E1 = self.E + 1
@@ -338,4 +344,4 @@ class SyntheticMoEStack(MoEStack):
                 self.dn_q[l, c0:c1], self.dn_s[l, c0:c1] = quantize_g128(w)
                 del w
         if prefill_tiles:
-            self.build_prefill_tiles()
+            self.build_prefill_tiles(gate_up_format)

@@ -111,11 +111,14 @@ def test_moe_layer_bounds_rejected_before_launch():
     assert fwd(16, ws, lay=hole) == _lib.LM_EINVAL
     assert b'null layer weight' in lib.lm_last_error()
     # a caller compiled against another layout of the struct is refused
-    assert layer.struct_size == ctypes.sizeof(_lib.MoeLayer) == 15 * 8  # the ENOMEM above: C agrees
+    assert layer.struct_size == ctypes.sizeof(_lib.MoeLayer) == 16 * 8  # the ENOMEM above: C agrees
     older = _lib.MoeLayer(*([fake] * 8), 0, 0, 0, 0)
-    older.struct_size = ctypes.sizeof(_lib.MoeLayer) - 16
+    older.struct_size = ctypes.sizeof(_lib.MoeLayer) - 8
     assert fwd(16, ws, lay=older) == _lib.LM_EINVAL
     assert b'struct_size' in lib.lm_last_error()
+    bad_fmt = _lib.MoeLayer(*([fake] * 8), 0, 0, 0, 0, None, None, 7)
+    assert fwd(16, ws, lay=bad_fmt) == _lib.LM_EINVAL
+    assert b'gu_q_tiles_format' in lib.lm_last_error()
 
 
 def test_workspace_regions():

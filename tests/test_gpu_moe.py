@@ -383,32 +383,83 @@ def test_prefill_weights_vs_exact_router(dev, capsys):
     assert rate < 1e-2
 
 
-def test_tile_rows_layout(dev):
+@pytest.mark.parametrize('fmt', [0, 1])
+def test_tile_rows_layout(dev, fmt):
     """lm_w8_tile_rows against the index formula of its declaration, on a
-    bank whose experts sit further apart than n * k (the stride is kept)."""
+    bank whose experts sit further apart than n * k (the stride is kept);
+    the fp16 format (1) also biases every byte by 128 and stores the bytes
+    of each 4-byte word in the order k = 0, 2, 1, 3."""
     from localmoe35ba3b_amd import _lib
     g = np.random.default_rng(7)
     E, n, k, es = 3, 48, 192, 48 * 192 + 1024
     flat = g.integers(-127, 128, size=E * es).astype(np.int8)
     q = torch.from_numpy(flat).to(dev)
     tiles = torch.zeros_like(q)
-    _lib.call('lm_w8_tile_rows', q.data_ptr(), E, n, k, es, tiles.data_ptr(), _lib.stream(dev))
+    _lib.call('lm_w8_tile_rows', q.data_ptr(), E, n, k, es, tiles.data_ptr(), fmt,
+              _lib.stream(dev))
     got = tiles.cpu().numpy()
     ref = np.zeros_like(flat)
     for e in range(E):
         w = flat[e * es:e * es + n * k].reshape(n // 16, 16, k // 64, 4, 16)  # b, r, s, p, j
-        ref[e * es:e * es + n * k] = w.transpose(0, 2, 3, 1, 4).reshape(-1)  # b, s, p, r, j
+        t = w.transpose(0, 2, 3, 1, 4).reshape(-1)  # b, s, p, r, j
+        if fmt == 1:
+            t = (t.view(np.uint8) ^ 0x80).reshape(-1, 4)[:, [0, 2, 1, 3]].reshape(-1).view(np.int8)
+        ref[e * es:e * es + n * k] = t
     assert np.array_equal(got, ref)
 
 
-def test_prefill_tiles_bit_identical(dev):
-    """The prefill GEMMs reading the tile-layout copy of the bank give the
-    same layer output and routing as reading the bank itself."""
+def f16_gate_up_model(xn, q, s):
+    """The fused layer's fp16 gate_up GEMM restated (not a reference
+    function): fp16 copies of the rows are exact and the MFMAs multiply them
+    by exact q, each group's scale acts on the fp32 sums, so up to fp32
+    summation the result is the float64 product with the unrounded weights
+    q * s (no bf16 rounding of q * s, unlike int8.py:21), rounded to bf16."""
+    w = q.astype(np.float64) * np.repeat(s.astype(np.float64), 128, axis=1)
+    return O.bf16((np.asarray(xn, np.float64) @ w.T).astype(np.float32))
+
+
+def test_prefill_tiles(dev, capsys):
+    """The prefill GEMMs on the tile-layout copies.  Plain copies give the
+    standard layout's result bit for bit.  The fp16 gate_up GEMM
+    (LM_TILES_F16) matches its own arithmetic restated in numpy (unrounded
+    q * s) to within a bf16 step or two on a few values, and the reference's
+    bf16(q * s) dequantization within the bf16 tolerance; routing is
+    unchanged."""
     st = SyntheticMoEStack(layers=1, seed=71, device=dev, max_tokens=2048, prefill_tiles=False)
     h = inputs(2048, 71, dev)
     plain, ids0, w0 = run_layer(st, h)
-    st.build_prefill_tiles()
+    plain_h = st.workspace_view('hidden', 2048).clone()
+    plain_rows = st.workspace_view('route_rows', 2048).cpu().numpy()  # run-dependent order
+    st.build_prefill_tiles(gate_up_format=0)  # both copies plain: bit for bit
+    assert torch.equal(run_layer(st, h)[0], plain)
+    st.build_prefill_tiles()  # gate_up's copy in the fp16 format (the default)
     tiled, ids1, w1 = run_layer(st, h)
     assert torch.equal(ids0, ids1) and torch.equal(w0, w1)
-    assert torch.equal(plain, tiled)
+    assert_close(npf(tiled), npf(plain), BF16_TOL, 'fp16 gate_up layer vs exact')
+    # the SwiGLU rows of one expert against both models
+    tiled_h = npf(st.workspace_view('hidden', 2048))
+    rows = st.workspace_view('route_rows', 2048).cpu().numpy()
+    idn = ids1.cpu().numpy()
+    e = int(idn[0, 0])
+    tok, slot = np.nonzero(idn == e)
+    r = rows[tok, slot]
+    xn = npf(st.workspace_view('normed', 2048))[tok]
+    q, sc = st.gu_q[0, e].cpu().numpy(), st.gu_s[0, e].cpu().numpy()
+    model = O.swiglu(f16_gate_up_model(xn, q, sc))
+    exact = O.swiglu(O.w8a16_linear(xn, q, sc))
+    same = np.sign(tiled_h[r]) * np.sign(model) >= 0
+    steps = np.abs(tiled_h[r].view(np.int32) - model.view(np.int32)) // 65536  # bf16 steps
+    assert same.mean() > 0.999 and np.median(steps) == 0 and steps[same].max() <= 2, (
+        f'{int((~same).sum())} sign flips, steps max {steps[same].max()}')
+    # SwiGLU rows are an intermediate: a one-step bf16 difference of a gate
+    # value times a large up value can exceed the elementwise bound, so they
+    # are held to the norm-wise bound; the layer output above is elementwise.
+    rel = np.linalg.norm(tiled_h[r] - exact) / np.linalg.norm(exact)
+    r0 = plain_rows[tok, slot]
+    rel_plain = np.linalg.norm(npf(plain_h)[r0] - exact) / np.linalg.norm(exact)
+    assert rel <= BF16_TOL and rel_plain <= BF16_TOL
+    with capsys.disabled():
+        print(f'\n[fp16 gate_up] expert {e}, {len(r)} rows: SwiGLU rel err vs exact dequant '
+              f'{rel:.2e} (bf16 path {rel_plain:.2e}); vs its fp16 model: '
+              f'{int((steps > 0).sum())} of {steps.size} values one bf16 step or more off')
     del st
