@@ -45,7 +45,7 @@ struct GemmArgs {
   const int8_t *q;
   int64_t q_es;
   const int8_t *q_tiles;  // q in the 16-row tile layout (weight load modes kWlTiles*)
-  const int *x_exp;       // kWlTilesF16: x row r holds fp16(x_r * 2^x_exp[r]) exactly
+  const int *x_exp;       // kWlTilesF16: x row r holds fp16(x_r * 2^x_exp[r])
   const float *s;
   int64_t s_es;
   uint16_t *y;
@@ -510,7 +510,8 @@ __device__ __forceinline__ void barrier_raw() { asm volatile("s_barrier" ::: "me
 //              a wave's load of one 16-row x 64-K block is 1 KB contiguous
 //              and lands in the MFMA layout, no permute.
 //   kWlTilesF16  the tile layout in its fp16 format (LM_TILES_F16) on fp16
-//              activation rows x_r = fp16(row r * 2^x_exp[r]) (exact): the
+//              activation rows x_r = fp16(row r * 2^x_exp[r]) (exact for the
+//              bf16 values of a normalized row down to 2^-31 of its norm): the
 //              MFMAs multiply exact fp16 q by the exact rows in fp16 with
 //              fp32 accumulation, and the group scales act on the
 //              accumulators.  Before the first MFMA of group g each

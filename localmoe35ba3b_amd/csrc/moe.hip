@@ -649,7 +649,6 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, c
   __shared__ float xf[kH];
   __shared__ float red[4];
   __shared__ float red2[4];
-  __shared__ float redm[4];
   __shared__ double dred[4];
   const int tok = blockIdx.x;
   const int t = threadIdx.x;
@@ -679,21 +678,12 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, c
     return;
   }
   norm_row_to_lds(ldg16(a.h + (int64_t)tok * kH + t * PER), nwv, a.eps, xf, red);
-  float am = 0.0f;
   {
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      ss += xf[t * PER + j] * xf[t * PER + j];
-      am = fmaxf(am, fabsf(xf[t * PER + j]));
-    }
+    for (int j = 0; j < PER; ++j) ss += xf[t * PER + j] * xf[t * PER + j];
     ss = wave_sum_f32(ss);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
-    if ((t & 63) == 0) {
-      red2[t >> 6] = ss;
-      redm[t >> 6] = am;
-    }
+    if ((t & 63) == 0) red2[t >> 6] = ss;
   }
   u32x4 packed;
 #pragma unroll
@@ -709,19 +699,19 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, c
   acc = wave_sum_f64_dpp(acc);
   if ((t & 63) == 0) dred[t >> 6] = acc;
   __syncthreads();
+  const float nxt = sqrtf((red2[0] + red2[1]) + (red2[2] + red2[3]));
   if (t == 0) {
     a.gl[tok] = round_bf16((float)(dred[0] + dred[1] + dred[2] + dred[3]));
-    a.nx[tok] = sqrtf((red2[0] + red2[1]) + (red2[2] + red2[3]));
+    a.nx[tok] = nxt;
   }
   // The fp16 copy of the row for the gate_up GEMM: xn * 2^k with the row's
-  // largest |value| in [2^14, 2^15).  A bf16 value with |v| 2^k >= 2^-17 is
-  // exact in fp16; smaller ones (below 2^-31 of the row maximum) round to the
-  // fp16 subnormal grid.
+  // Euclidean norm (which bounds every |value|) in [2^14, 2^15).  A bf16
+  // value with |v| 2^k >= 2^-17 is exact in fp16; smaller ones (below 2^-31
+  // of the norm) round to the fp16 subnormal grid.
   {
     int ex = 0;
-    const float m = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
-    (void)frexpf(m, &ex);
-    const int k = m > 0.0f ? min(max(15 - ex, -126), 126) : 0;
+    (void)frexpf(nxt, &ex);
+    const int k = nxt > 0.0f ? min(max(15 - ex, -126), 126) : 0;
     u32x4 hp;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
