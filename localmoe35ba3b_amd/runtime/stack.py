@@ -317,13 +317,15 @@ class MoEStack:
 class SyntheticMoEStack(MoEStack):
     """Random-init 35B-A3B-class MoE-FFN stack resident in HBM: weights drawn
     on the GPU from per-(layer, matrix) seeds, N(0, 0.02) fp32, quantized by
-    the group-128 HIP quantizer; RMSNorm weight zero.  With prefill_tiles the
+    the group-128 HIP quantizer; RMSNorm weight zero (norm=True allocates a
+    zero weight tensor the caller may fill, norm_w).  With prefill_tiles the
     prefill GEMMs read a tile-layout copy of the int8 bank, gate_up's in
     `gate_up_format` (build_prefill_tiles)."""
 
     def __init__(self, layers=40, seed=4, device='cuda', max_tokens=2048, router_bias=None,
-                 chunk_experts=32, prefill_tiles=True, gate_up_format=_lib.LM_TILES_F16):
-        super().__init__(layers, device, max_tokens, router_bias)
+                 chunk_experts=32, prefill_tiles=True, gate_up_format=_lib.LM_TILES_F16,
+                 norm=False):
+        super().__init__(layers, device, max_tokens, router_bias, norm)
         dev = self.device
         E1 = self.E + 1
         gen = torch.Generator(device=dev)

@@ -137,7 +137,8 @@ def w8a16_linear(x, q, s, round_to=bf16):
 # ----------------------------------------------------------------- a11 SwiGLU
 def silu_f32(g):
     g = np.asarray(g, np.float32)
-    return (g / (np.float32(1) + np.exp(-g))).astype(np.float32)
+    with np.errstate(over='ignore'):  # exp(-g) = inf for g < -88 gives the limit -0
+        return (g / (np.float32(1) + np.exp(-g))).astype(np.float32)
 
 
 def swiglu(gu, round_to=bf16):
@@ -320,7 +321,8 @@ def moe_block(x, layer, k=8, w8a8_routed=None, routing=None):
     sh = expert_w8a16(x, layer['gu_q'][e_routed], layer['gu_s'][e_routed],
                       layer['dn_q'][e_routed], layer['dn_s'][e_routed])
     gl = router_logits(x, layer['shared_gate_w'][None, :])[:, 0]
-    sig = bf16((np.float32(1) / (np.float32(1) + np.exp(-gl))).astype(np.float32))
+    with np.errstate(over='ignore'):  # exp(-gl) = inf gives the limit 0
+        sig = bf16((np.float32(1) / (np.float32(1) + np.exp(-gl))).astype(np.float32))
     out = bf16(routed + bf16(sig[:, None] * sh))
     return out, (lg, wts, ids)
 

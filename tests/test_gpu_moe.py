@@ -272,6 +272,60 @@ def test_zipf_chunk_2048(dev):
         assert torch.equal(static, out), f'replay {i}'
 
 
+def f16_expert(x, gu_q, gu_s, dn_q, dn_s, round_to=O.bf16):
+    """O.expert_w8a16 with the gate_up of the fused layer's fp16 path
+    (f16_gate_up_model: unrounded q * s) and the reference's down."""
+    return O.w8a16_linear(O.swiglu(f16_gate_up_model(x, gu_q, gu_s)), dn_q, dn_s, round_to)
+
+
+@pytest.mark.parametrize('fmt', [0, 1])
+def test_prefill_extreme_inputs(dev, fmt, monkeypatch):
+    """The prefill path on inputs at the edges of its number formats, with
+    both gate_up tile formats: RMSNorm weights that put normalized values
+    far beyond fp16's range (the fp16 row copy is scaled by a power of two
+    from the row norm), a token row 10^6 times smaller than the others, a
+    routed expert with all-zero weight groups (scale 1e-30, the quantizer's
+    floor) and groups with scales of 1e-3 and 1e3 times their neighbours'.
+    Routing is exact and the layer output stays within the bf16 tolerance
+    of the oracle (norm-wise for the fp16 path, whose skipped bf16 rounding
+    of q * s exceeds the elementwise bound on a few hundred of the large,
+    cancelling outputs here; elementwise against a model of its own
+    arithmetic)."""
+    st = SyntheticMoEStack(layers=1, seed=91, device=dev, max_tokens=256, norm=True,
+                           gate_up_format=fmt)
+    g = torch.Generator(device=dev)
+    g.manual_seed(92)
+    w = torch.randn(2048, generator=g, device=dev) * 0.5
+    w[::97] = 3000.0  # (1 + w) up to 3001: |xn| up to ~1.4e5 on those channels
+    st.norm_w[0].copy_(w)
+    h = inputs(256, 93, dev)
+    h[7] *= 1e-6
+    # pick an expert that the routing uses, then damage its weights
+    _, ids, _ = run_layer(st, h)
+    e = int(ids[0, 0])
+    st.gu_q[0, e, :, :128] = 0
+    st.gu_s[0, e, :, 0] = 1e-30
+    st.gu_s[0, e, :512, 3] *= 1e-3
+    st.gu_s[0, e, 512:, 5] *= 1e3
+    st.dn_q[0, e, :, 128:256] = 0
+    st.dn_s[0, e, :, 1] = 1e-30
+    st.build_prefill_tiles(fmt)
+    out, ids, wts = run_layer(st, h)
+    torch.cuda.synchronize()
+    ref, (_, rw, ri) = oracle_layer(st, npf(h), 0, ids.cpu().numpy())
+    assert np.array_equal(ids.cpu().numpy(), ri)
+    assert np.abs(npf(wts) - rw).max() <= 2.0 ** -8
+    assert np.isfinite(npf(out)).all()
+    if fmt == 0:
+        assert_close(npf(out), ref, BF16_TOL, 'extreme inputs, exact gate_up')
+        return
+    rel = np.linalg.norm(npf(out) - ref) / np.linalg.norm(ref)
+    assert rel <= BF16_TOL, rel
+    monkeypatch.setattr(O, 'expert_w8a16', f16_expert)
+    model, _ = oracle_layer(st, npf(h), 0, ids.cpu().numpy())
+    assert_close(npf(out), model, BF16_TOL, 'extreme inputs, fp16 gate_up vs its model')
+
+
 def test_tile_copy_stale_weights_refused(dev):
     """Writing gu_q or dn_q in place after build_prefill_tiles leaves the
     prefill tile copies stale: the stack refuses to run until they are
