@@ -671,6 +671,11 @@ def main():
         'decode_hbm_gbs': round(decode_gbs, 1),
         'decode_hbm_frac': round(decode_gbs / HBM_PEAK_GBS, 4),
         'decode_dtype': 'int8 (W8A8 experts), bf16 (shared expert, router fp64)',
+        'prefill_dtype': ('bf16 activations and outputs; gate_up on fp16 MFMAs (exact q, exact '
+                          'fp16 copies of the rows, group scales on the fp32 sums), down on bf16 '
+                          'MFMAs of bf16(q*s); router fp64/bf16'
+                          if stack._structs[0].gu_q_tiles_format == 1 and stack.gu_q_tiles is not None
+                          else 'bf16 MFMAs of bf16(q*s), fp32 accumulation; router fp64/bf16'),
         'mean_active_experts': round(mean_active, 1),
         'roofline': roofline,
         'kernels': kernels,

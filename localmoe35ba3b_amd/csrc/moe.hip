@@ -704,11 +704,12 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, c
     a.gl[tok] = round_bf16((float)(dred[0] + dred[1] + dred[2] + dred[3]));
     a.nx[tok] = nxt;
   }
-  // The fp16 copy of the row for the gate_up GEMM: xn * 2^k with the row's
-  // Euclidean norm (which bounds every |value|) in [2^14, 2^15).  A bf16
-  // value with |v| 2^k >= 2^-17 is exact in fp16; smaller ones (below 2^-31
-  // of the norm) round to the fp16 subnormal grid.
-  {
+  // The fp16 copy of the row for the gate_up GEMM on fp16 tiles (xh is null
+  // otherwise): xn * 2^k with the row's Euclidean norm (which bounds every
+  // |value|) in [2^14, 2^15).  A bf16 value with |v| 2^k >= 2^-17 is exact in
+  // fp16; smaller ones (below 2^-31 of the norm) round to the fp16 subnormal
+  // grid.
+  if (a.xh) {
     int ex = 0;
     (void)frexpf(nxt, &ex);
     const int k = nxt > 0.0f ? min(max(15 - ex, -126), 126) : 0;
@@ -1294,7 +1295,7 @@ extern "C" int lm_moe_workspace_init(void *workspace, int64_t bytes, void *strea
 // host threads) race.  No region needs a starting value: every call writes
 // each region before reading it.
 constexpr int64_t kScratchMaxTokens = 128;
-constexpr int64_t kScratchBytes = layout(kScratchMaxTokens).total;  // about 6.7 MB
+constexpr int64_t kScratchBytes = layout(kScratchMaxTokens).total;  // 7,219,968 B
 __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
@@ -1368,7 +1369,11 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   a.h = static_cast<uint16_t *>(h);
   a.eps = eps;
   a.xn = reinterpret_cast<uint16_t *>(ws + w.xn);
-  a.xh = reinterpret_cast<uint16_t *>(ws + w.xh);
+  // With an LM_TILES_F16 copy of gu_q the prefill gate_up GEMM runs in fp16
+  // on xh (exact copies of the normalized rows, written by the norm kernel);
+  // otherwise in bf16 on xn.
+  const bool f16 = layer->gu_q_tiles != nullptr && layer->gu_q_tiles_format == LM_TILES_F16;
+  a.xh = f16 ? reinterpret_cast<uint16_t *>(ws + w.xh) : nullptr;
   a.xk = reinterpret_cast<int *>(ws + w.xk);
   a.gl = reinterpret_cast<float *>(ws + w.gl);
   a.logits = reinterpret_cast<float *>(ws + w.logits);
@@ -1438,9 +1443,6 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   // gate_up over the T token rows gathered through pos, down over the R + T
   // rows of hbuf; the banks hold E + 1 experts (index E = shared expert)
   // (the weights' tile-layout copies, when the caller provides them)
-  // With an LM_TILES_F16 copy of gu_q the GEMM runs in fp16 on xh (exact
-  // copies of the normalized rows); otherwise in bf16 on xn.
-  const bool f16 = layer->gu_q_tiles != nullptr && layer->gu_q_tiles_format == LM_TILES_F16;
   const RoutedGemm gu{f16 ? a.xh : a.xn, kH,  T,  a.gu_q, a.gu_s,  a.gu_qes, a.gu_ses,
                       kE + 1,  pos,     table, w.n_tiles, kBM, a.hbuf, R + T,
                       2 * kI,  kH,      true,  true,   LM_BF16, layer->gu_q_tiles,
