@@ -46,6 +46,7 @@ struct GemmArgs {
   int64_t q_es;
   const int8_t *q_tiles;  // q in the 16-row tile layout (weight load modes kWlTiles*)
   const int *x_exp;       // kWlTilesF16: x row r holds fp16(x_r * 2^x_exp[r])
+  const int *ptile;       // gathered tile GEMMs: x row of tile row r of table row i at i * tile_rows + r
   const float *s;
   int64_t s_es;
   uint16_t *y;
@@ -547,7 +548,7 @@ __device__ __forceinline__ int rb_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); 
 template <typename T, bool SWIGLU, bool GATHER, int WL, int K, int BM, int TN, int BD, int HL, int AD,
           int NW, int MS>
 __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t start, int rows,
-                                        int nt, unsigned char *smem) {
+                                        int nt, unsigned char *smem, const int *gx, int gk) {
   constexpr int KS = 64 * HL;
   constexpr int KT = K / KS;
   constexpr int G = K / 128;
@@ -635,13 +636,18 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   }
   // Activation sources: wave-load j fills rows RPL (4 j + wave) ..; lane ->
   // row RPL (4 j + wave) + lane / CPR, LDS chunk lane % CPR, which holds the
-  // logical chunk (lane % CPR) ^ (row & 7).
+  // logical chunk (lane % CPR) ^ (row & 7).  Gathered rows on the tile
+  // copies come from the tile-major map (gx, requested by the caller with
+  // the table row), rows past the tile's end from x row 0; otherwise from
+  // pos, rows past the end re-reading the tile's last row.
+  constexpr bool PT = GATHER && TILES;
   const uint16_t *asrc[A_W];
 #pragma unroll
   for (int j = 0; j < A_W; ++j) {
     const int r = RPL * (NW * j + wave) + lane / CPR;
     const int rr = min(r, rows - 1);
-    const int64_t xr = GATHER ? clamp_index(a.pos[start + rr], a.x_rows) : start + rr;
+    const int64_t xr = GATHER ? clamp_index(PT ? (r < rows ? gx[j] : 0) : a.pos[start + rr], a.x_rows)
+                              : start + rr;
     asrc[j] = a.x + xr * a.ldx + (((lane % CPR) ^ rb_swz(r)) * 8);
   }
   // kWlTilesF16: thread t < BM fetches the exponent of tile row t (consumed
@@ -649,7 +655,8 @@ __device__ __forceinline__ void rb_tile(const GemmArgs &a, int64_t e, int64_t st
   int rk = 0;
   if constexpr (F16) {
     const int rr = min(tid, rows - 1);
-    rk = a.x_exp[GATHER ? clamp_index(a.pos[start + rr], a.x_rows) : start + rr];
+    rk = a.x_exp[GATHER ? clamp_index(PT ? (tid < rows ? gk : 0) : a.pos[start + rr], a.x_rows)
+                        : start + rr];
   }
 
   u32x4 breg[BD][NI][HL];
@@ -874,6 +881,26 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
   __shared__ __align__(16) unsigned char smem[3 * BM * 128 * HL + SC_BYTES];
   int mt, nt;
   if (!xcd_tile(a, mt, nt)) return;
+  // Gathered rows on the tile copies: this tile's rows of the tile-major
+  // gather map, requested before the table row and independently of it
+  // (the rows rb_tile assigns to this lane for the tallest tile, and to
+  // thread t < BM for the row exponents), so the activation loads wait for
+  // one dependent load instead of two.
+  constexpr bool PT = GATHER && (WL == kWlTiles || WL == kWlTilesF16);
+  constexpr int RPL = 8 / HL, CPR = 8 * HL;
+  constexpr int AWM = (BM / RPL + NW - 1) / NW;
+  static_assert(NW * AWM * RPL <= BM, "gather map rows inside the tile");
+  int gx[AWM];
+  int gk = 0;
+#pragma unroll
+  for (int j = 0; j < AWM; ++j) gx[j] = 0;
+  if constexpr (PT) {
+    const int *pt = a.ptile + (int64_t)mt * a.tile_rows;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < AWM; ++j) gx[j] = pt[RPL * (NW * j + wave) + lane / CPR];
+    if constexpr (WL == kWlTilesF16) gk = pt[min((int)threadIdx.x, BM - 1)];
+  }
   int64_t e = 0, start;
   int rows;
   if (a.table) {
@@ -889,13 +916,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
   if (rows <= 0) return;
   static_assert(BM == 96, "row-count dispatch below covers 96-row tiles");
   if (rows > 80)
-    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 6>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 6>(a, e, start, rows, nt, smem, gx, gk);
   else if (rows > 64)
-    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 5>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 5>(a, e, start, rows, nt, smem, gx, gk);
   else if (rows > 32)
-    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 4>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 4>(a, e, start, rows, nt, smem, gx, gk);
   else
-    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem);
+    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem, gx, gk);
 }
 
 // Configuration of grouped_rb_kernel, chosen by measurement on the
@@ -1025,12 +1052,15 @@ int routed_gemm(const RoutedGemm &r, hipStream_t st) {
   a.q_es = r.q_es;
   a.q_tiles = r.q_tiles;
   a.x_exp = r.x_exp;
+  a.ptile = r.ptile;
   a.s = r.s;
   a.s_es = r.s_es;
   a.y = static_cast<uint16_t *>(r.y);
   a.ldy = r.swiglu ? r.n / 2 : r.n;
   LM_REQUIRE(!r.q_tiles || (r.n % 32 == 0 && r.k % 64 == 0), LM_EINVAL,
              "the tile layout needs n % 32 == 0 and k % 64 == 0");
+  LM_REQUIRE(!r.q_tiles || !r.gather || (r.ptile && r.bm == 96), LM_EINVAL,
+             "gathered rows on the tile layout need the tile-major gather map of 96-row tiles");
   LM_REQUIRE(!r.x_exp || (r.q_tiles && r.dtype == LM_BF16 && r.bm <= 96 &&
                           (r.k == 2048 || r.k == 512)),
              LM_EINVAL, "fp16 rows need LM_TILES_F16 weights, bf16 output, tiles <= 96 rows "

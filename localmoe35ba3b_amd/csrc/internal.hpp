@@ -34,6 +34,10 @@ struct RoutedGemm {
   // Non-null: x holds fp16 rows fp16(row r * 2^x_exp[r]) (exact) and q_tiles
   // is in the LM_TILES_F16 format; the output is bf16.
   const int *x_exp = nullptr;
+  // Gathered GEMMs on q_tiles: the token of row r of table tile i at
+  // ptile[i * bm + r] (any value for rows past the tile's end), read with the
+  // table row instead of through pos; required with q_tiles and gather.
+  const int *ptile = nullptr;
 };
 int routed_gemm(const RoutedGemm &r, hipStream_t st);
 

@@ -36,7 +36,7 @@ static_assert(kE == 256, "the prefill kernels map one thread of a 256-thread wor
 
 struct WsLayout {
   int64_t bcounts, xn, xh, xk, gl, logits, nx, nw, ids, wts, sel, selw, xq, xs, dacc_gu, dacc_dn,
-      pos, table, rslot, rpos, hbuf, vbuf, total;
+      pos, table, ptile, rslot, rpos, hbuf, vbuf, total;
   int64_t max_tiles, n_tiles;
 };
 
@@ -70,6 +70,7 @@ constexpr WsLayout layout(int64_t T) {
   w.dacc_dn = take(kTopK * kH * 4);      // decode: fp32 W8A8 sums of the routed down rows
   w.pos = take((R + T) * 8);
   w.table = take(w.n_tiles * 3 * 8);
+  w.ptile = take(w.n_tiles * kBM * 4);  // token of row r of table tile i at i * kBM + r
   w.bcounts = take((T + kTopkTokens - 1) / kTopkTokens * kE);  // per top-k workgroup expert counts (bytes)
   w.rslot = take(R * 4);  // rank of each route inside its top-k workgroup and expert
   w.rpos = take(R * 4);   // sorted row of each route
@@ -1039,7 +1040,10 @@ __global__ __launch_bounds__(kTopkTokens * 64) void prefill_topk_count_kernel(
 // columns itself (nb rows of kE byte counts, 64 KB for 2048 tokens), so no
 // grid-wide step is needed.  Workgroup 0 also writes the tile table (the
 // shared expert's tiles over rows [R, R + T), then kBM-row tiles per routed
-// expert, then surplus rows (0, 0, 0)) and the shared rows' tokens.
+// expert, then surplus rows (0, 0, 0)) and the shared rows' tokens.  Every
+// route's token also goes to the tile-major gather map ptile (row r of
+// table tile i at i * kBM + r; every workgroup scans the tile counts), which
+// the gate_up GEMM reads together with its table row rather than after it.
 //
 // Every load of a phase is issued unconditionally (clamped rows), so the
 // phase pays one load latency, not one per row.
@@ -1049,11 +1053,12 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
                                                             int nb, int T, int max_tiles,
                                                             int64_t *__restrict__ pos,
                                                             int64_t *__restrict__ table,
+                                                            int *__restrict__ ptile,
                                                             int *__restrict__ rpos) {
   constexpr int Q = 16;  // row phases: wave q sums rows q, q + Q, ...
   static_assert(kE == 4 * 64, "a lane sums 4 experts' byte counts");
   __shared__ int ptot[Q][kE], ppre[Q][kE], bpre[kScanGroups][kE];
-  __shared__ int offs[kE + 1], scratch[4];
+  __shared__ int offs[kE + 1], toffs[kE], scratch[4];
   const int t = threadIdx.x;
   const int R = T * kTopK;
   const int r = blockIdx.x * kScanRoutes + t;
@@ -1114,7 +1119,15 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
   };
   int all = 0;
   const int ex = scan(c, &all);
-  if (t < kE) offs[t] = ex;
+  // tiles: the shared expert's nst first, then expert e's nt at nst + tex
+  const int nst = (T + kBM - 1) / kBM;
+  const int nt = t < kE ? (c + kBM - 1) / kBM : 0;
+  int ntot = 0;
+  const int tex = scan(nt, &ntot);
+  if (t < kE) {
+    offs[t] = ex;
+    toffs[t] = tex;
+  }
   if (t == 0) offs[kE] = all;
   __syncthreads();
   if (r < R) {
@@ -1122,16 +1135,15 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
     const int p = clamp_index32(offs[e_r] + bpre[jb][e_r] + s_r, R);
     pos[p] = r / kTopK;
     rpos[r] = p;
+    const int q = max(p - offs[e_r], 0);  // rank among the expert's routes
+    const int tile = clamp_index32(nst + toffs[e_r] + q / kBM, nst + max_tiles);
+    ptile[(int64_t)tile * kBM + q % kBM] = r / kTopK;
   }
   if (blockIdx.x != 0) return;
   // Tile table: the shared expert's nst full tiles over rows [R, R + T)
   // first (the longest tiles start first), then thread e writes the tiles of
   // routed expert e at nst + its exclusive tile prefix, and rows past the
   // last tile up to nst + max_tiles are (0, 0, 0).
-  const int nst = (T + kBM - 1) / kBM;
-  const int nt = t < kE ? (c + kBM - 1) / kBM : 0;
-  int ntot = 0;
-  const int tex = scan(nt, &ntot);
   for (int k = 0; k < nt; ++k) {
     const int64_t i = nst + tex + k;
     table[i * 3] = t;
@@ -1148,7 +1160,10 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
     table[(int64_t)j * 3 + 1] = R + (int64_t)j * kBM;
     table[(int64_t)j * 3 + 2] = R + T;
   }
-  for (int tok = t; tok < T; tok += 1024) pos[R + tok] = tok;
+  for (int tok = t; tok < T; tok += 1024) {
+    pos[R + tok] = tok;
+    ptile[tok] = tok;  // shared tile j, row r: token j * kBM + r
+  }
 }
 
 // Per token: routed combine in ascending expert order, gated shared add,
@@ -1418,6 +1433,7 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   const int64_t T = tokens, R = T * kTopK;
   int64_t *pos = reinterpret_cast<int64_t *>(ws + w.pos);
   int64_t *table = reinterpret_cast<int64_t *>(ws + w.table);
+  int *ptile = reinterpret_cast<int *>(ws + w.ptile);
   uint8_t *bcounts = ws + w.bcounts;
   int *rslot = reinterpret_cast<int *>(ws + w.rslot);
   int *rpos = reinterpret_cast<int *>(ws + w.rpos);
@@ -1437,7 +1453,8 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   if (int rc = check_launch("prefill_topk_count_kernel")) return rc;
   if (int rc = mark(3)) return rc;
   prefill_scan_kernel<<<cdiv(R, kScanRoutes), 1024, 0, st>>>(a.ids, rslot, bcounts, nb, (int)T,
-                                                              (int)w.max_tiles, pos, table, rpos);
+                                                              (int)w.max_tiles, pos, table, ptile,
+                                                              rpos);
   if (int rc = check_launch("prefill_scan_kernel")) return rc;
   if (int rc = mark(4)) return rc;
   // gate_up over the T token rows gathered through pos, down over the R + T
@@ -1446,7 +1463,7 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   const RoutedGemm gu{f16 ? a.xh : a.xn, kH,  T,  a.gu_q, a.gu_s,  a.gu_qes, a.gu_ses,
                       kE + 1,  pos,     table, w.n_tiles, kBM, a.hbuf, R + T,
                       2 * kI,  kH,      true,  true,   LM_BF16, layer->gu_q_tiles,
-                      f16 ? a.xk : nullptr};
+                      f16 ? a.xk : nullptr, ptile};
   if (int rc = routed_gemm(gu, st)) return rc;
   if (int rc = mark(5)) return rc;
   const RoutedGemm dn{a.hbuf,  kI,      R + T, a.dn_q, a.dn_s, a.dn_qes, a.dn_ses,
