@@ -914,15 +914,26 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
     rows = (int)min((int64_t)a.tile_rows, a.M - start);
   }
   if (rows <= 0) return;
-  static_assert(BM == 96, "row-count dispatch below covers 96-row tiles");
-  if (rows > 80)
-    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 6>(a, e, start, rows, nt, smem, gx, gk);
-  else if (rows > 64)
-    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 5>(a, e, start, rows, nt, smem, gx, gk);
-  else if (rows > 32)
-    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 4>(a, e, start, rows, nt, smem, gx, gk);
-  else
-    rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem, gx, gk);
+  if constexpr (BM == 128) {  // dense rows at M >= kDenseTallM
+    if (rows > 96)
+      rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 8>(a, e, start, rows, nt, smem, gx, gk);
+    else if (rows > 64)
+      rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 6>(a, e, start, rows, nt, smem, gx, gk);
+    else if (rows > 32)
+      rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 4>(a, e, start, rows, nt, smem, gx, gk);
+    else
+      rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem, gx, gk);
+  } else {
+    static_assert(BM == 96, "row-count dispatch below covers 96-row tiles");
+    if (rows > 80)
+      rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 6>(a, e, start, rows, nt, smem, gx, gk);
+    else if (rows > 64)
+      rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 5>(a, e, start, rows, nt, smem, gx, gk);
+    else if (rows > 32)
+      rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 4>(a, e, start, rows, nt, smem, gx, gk);
+    else
+      rb_tile<T, SWIGLU, GATHER, WL, K, BM, TN, BD, HL, AD, NW, 2>(a, e, start, rows, nt, smem, gx, gk);
+  }
 }
 
 // Configuration of grouped_rb_kernel, chosen by measurement on the
@@ -934,7 +945,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void grouped_rb_kernel(GemmArgs a) {
 // half as often as with 32 columns.  On the 40-layer stack, two chunks
 // overlapped, that is 3 % more prefill tokens/s, though each GEMM alone is
 // 1-2 % slower (and 8 % on a Zipf-skewed chunk, whose hot expert is compute
-// bound at the lower occupancy).  Every other use keeps 32 columns at 3 per CU.
+// bound at the lower occupancy).  Every other use keeps 32 columns at 3 per CU,
+// except dense matrices of at least kDenseTallM rows: 128-row tiles, so each
+// dequantized weight feeds 8 row sub-tiles instead of 6, with activations 3
+// stages ahead (56 KB of LDS: 2 workgroups per CU).  At M = 2048 (512 tiles,
+// the chip's 512 slots) that is 44.5-46.4 us against 50.5-51.5 us; below
+// M = 1024 the 96-row tiles are faster (25 against 29 us at M = 256, where
+// each tile's 32 stages set the time).
 constexpr int kRbTN = 32;
 constexpr int kRbOcc = 3;
 constexpr int kRbTnTiles = 64;
@@ -944,18 +961,24 @@ constexpr int kRbHL = 1;
 constexpr int kRbAD = 2;
 constexpr int kRbNW = 4;
 constexpr int kGroupedBN = 128;  // grouped_mfma_kernel tile columns
+constexpr int kRbBMTall = 128;
+constexpr int kRbADTall = 3;
+constexpr int64_t kDenseTallM = 1024;
 
-template <typename T, bool SWIGLU, bool GATHER, int WL, int K>
+template <typename T, bool SWIGLU, bool GATHER, int WL, int K, int BM = 96>
 static int launch_rb(GemmArgs a, unsigned mtiles, hipStream_t st) {
   constexpr bool TILES = WL == kWlTiles || WL == kWlTilesF16;
+  constexpr bool TALL = BM == kRbBMTall;
+  static_assert(!TALL || (WL == kWlDirect && !SWIGLU && !GATHER), "tall tiles serve dense rows");
   constexpr int TN = TILES ? kRbTnTiles : kRbTN;
-  constexpr int OCC = TILES ? kRbOccTiles : kRbOcc;
+  constexpr int OCC = TILES || TALL ? kRbOccTiles : kRbOcc;
+  constexpr int AD = TALL ? kRbADTall : kRbAD;
   constexpr int RBN = kRbNW * TN;
   a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, RBN / 2) : (int)cdiv(a.N, RBN);
   a.mt_count = (int)mtiles;
   const int64_t grid = xcd_grid(a.mt_count, a.nt_count);
   LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
-  grouped_rb_kernel<T, SWIGLU, GATHER, WL, K, 96, TN, kRbBD, kRbHL, kRbAD, kRbNW, OCC>
+  grouped_rb_kernel<T, SWIGLU, GATHER, WL, K, BM, TN, kRbBD, kRbHL, AD, kRbNW, OCC>
       <<<(unsigned)grid, kRbNW * 64, 0, st>>>(a);
   return check_launch("grouped_rb_kernel");
 }
@@ -965,6 +988,11 @@ static int launch_rb(GemmArgs a, unsigned mtiles, hipStream_t st) {
 template <typename T, bool SWIGLU, bool GATHER, int WL>
 static int launch_grouped(GemmArgs a, unsigned mtiles, hipStream_t st) {
   if (mtiles == 0) return LM_OK;
+  if constexpr (WL == kWlDirect && !SWIGLU && !GATHER) {
+    if (!a.table && a.tile_rows == kRbBMTall && (a.K == 2048 || a.K == 512))
+      return a.K == 2048 ? launch_rb<T, false, false, WL, 2048, kRbBMTall>(a, mtiles, st)
+                         : launch_rb<T, false, false, WL, 512, kRbBMTall>(a, mtiles, st);
+  }
   if (a.tile_rows <= 96 && (a.K == 2048 || a.K == 512))
     return a.K == 2048 ? launch_rb<T, SWIGLU, GATHER, WL, 2048>(a, mtiles, st)
                        : launch_rb<T, SWIGLU, GATHER, WL, 512>(a, mtiles, st);
@@ -1003,12 +1031,14 @@ int w8a16_gemm_dense(const void *x, const int8_t *q, const float *s, void *y, in
   a.K = (int)k;
   (void)large_tile;
   // Rows at the model's K: the register-streamed kernel over 96-row tiles of
-  // the dense matrix (no tile table), faster than the LDS-dequant kernel
-  // because each wave dequantizes only its own columns' weights.
+  // the dense matrix (128-row tiles from kDenseTallM rows; no tile table),
+  // faster than the LDS-dequant kernel because each wave dequantizes only
+  // its own columns' weights.
   if (k == 2048 || k == 512) {
-    a.tile_rows = 96;
-    return dtype == LM_BF16 ? launch_grouped<BF16, false, false, kWlDirect>(a, cdiv(m, 96), st)
-                            : launch_grouped<FP16, false, false, kWlDirect>(a, cdiv(m, 96), st);
+    const int bm = m >= kDenseTallM ? kRbBMTall : 96;
+    a.tile_rows = bm;
+    return dtype == LM_BF16 ? launch_grouped<BF16, false, false, kWlDirect>(a, cdiv(m, bm), st)
+                            : launch_grouped<FP16, false, false, kWlDirect>(a, cdiv(m, bm), st);
   }
   const unsigned mt = cdiv(m, 128);
   if (dtype == LM_BF16) return launch_gemm<BF16, 128, 2, false, false, true>(a, mt, st);

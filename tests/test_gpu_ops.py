@@ -153,8 +153,12 @@ def test_w8a8_grouped_decode_bit_exact(dev):
 
 # ------------------------------------------------------------- a2 W8A16
 @pytest.mark.parametrize('m,n,k', [(1, 4096, 2048), (2048, 4096, 2048), (3, 1000, 384),
-                                   (37, 1000, 384), (8, 512, 2048), (130, 2048, 512)])
+                                   (37, 1000, 384), (8, 512, 2048), (130, 2048, 512),
+                                   (1057, 4096, 2048), (1100, 1000, 512)])
 def test_w8a16_linear(dev, m, n, k):
+    """Every GEMM path of int8.linear against the oracle: the GEMV (m <= 8),
+    96-row tiles, 128-row tiles from m = 1024 (1057 and 1100 end in partial
+    tiles of 33 and 76 rows), the generic kernel at K = 384."""
     gen = seeded(m + n)
     x = bf16_rand((m, k), gen)
     wq, ws = O.quantize_weight((torch.randn(n, k, generator=gen) * 0.02).numpy())
@@ -162,7 +166,7 @@ def test_w8a16_linear(dev, m, n, k):
     assert_close(npf(y), O.w8a16_linear(npf(x), wq, ws), BF16_TOL, f'w8a16 {m}x{n}x{k}')
 
 
-@pytest.mark.parametrize('m', [1, 5, 300])
+@pytest.mark.parametrize('m', [1, 5, 300, 1030])
 def test_w8a16_linear_exact(dev, m):
     """Integer activations and power-of-two scales make every product and sum
     exact in fp32, so any MFMA/GEMV layout or dequant error shows bit for bit."""
@@ -177,9 +181,10 @@ def test_w8a16_linear_exact(dev, m):
     assert np.array_equal(npf(y), O.bf16(exact.astype(np.float32)))
 
 
-def test_w8a16_linear_fp16(dev):
+@pytest.mark.parametrize('m', [64, 1030])
+def test_w8a16_linear_fp16(dev, m):
     gen = seeded(5)
-    x = (torch.randn(64, 512, generator=gen)).to(torch.float16)
+    x = (torch.randn(m, 512, generator=gen)).to(torch.float16)
     wq, ws = O.quantize_weight((torch.randn(256, 512, generator=gen) * 0.02).numpy())
     y = int8.linear(x.to(dev), torch.from_numpy(wq).to(dev), torch.from_numpy(ws).to(dev))
     wd = O.dequant(wq, ws, lambda a: a.astype(np.float16).astype(np.float32))
