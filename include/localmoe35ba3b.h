@@ -363,7 +363,7 @@ int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t tokens,
                          void *stream);
 
 /* lm_moe_layer_forward without a workspace argument: the call's workspace
- * is a device array inside the library (one per device, about 7.2 MB, held
+ * is a device array inside the library (one per device, about 7.3 MB, held
  * until the process ends), so the call allocates nothing and takes no
  * scratch from the caller.  It may be captured in a HIP graph once
  * lm_moe_static_init() has run on the device.  No counterpart in the

@@ -1310,7 +1310,7 @@ extern "C" int lm_moe_workspace_init(void *workspace, int64_t bytes, void *strea
 // host threads) race.  No region needs a starting value: every call writes
 // each region before reading it.
 constexpr int64_t kScratchMaxTokens = 128;
-constexpr int64_t kScratchBytes = layout(kScratchMaxTokens).total;  // 7,219,968 B
+constexpr int64_t kScratchBytes = layout(kScratchMaxTokens).total;  // 7,323,392 B
 __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
