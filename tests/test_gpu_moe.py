@@ -57,8 +57,11 @@ def test_decode_layer(stack, dev, seed):
     assert_close(npf(out), ref, BF16_TOL, 'decode layer')
 
 
-@pytest.mark.parametrize('tokens', [2, 67])
+@pytest.mark.parametrize('tokens', [2, 67, 96, 97, 192])
 def test_prefill_layer(stack, dev, tokens):
+    """One prefill layer against the oracle; 96, 97 and 192 tokens put the
+    shared expert's rows on and just past whole 96-row tiles of the
+    tile-major gather map."""
     h = inputs(tokens, 100 + tokens, dev)
     out, ids, wts = run_layer(stack, h)
     ref, (lg, rw, ri) = oracle_layer(stack, npf(h), 0, ids.cpu().numpy())
