@@ -362,6 +362,29 @@ int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t tokens,
                          void *weights_out, void *const *phase_events,
                          void *stream);
 
+/* lm_moe_layer_forward for consecutive layers of one prefill chunk on one
+ * workspace (the stack loop of HF:866-875 applied layer after layer).  With
+ * next != NULL, the call's last kernel (the combine) also does next's norm
+ * work on the rows it has just written: RMSNorm with next->norm_w, next's
+ * shared-gate logit, the norms of next's router rows and, when next's
+ * gate_up tiles are LM_TILES_F16, the fp16 row copy - the same code and
+ * order as next's own norm kernel, so the results are bit-identical to
+ * unchained calls.  The next call, on the same rows, workspace, stream and
+ * eps with layer == this call's next, passes input_normed = 1 and skips its
+ * norm kernel.  After a call with next, the LM_WS_NORMED and LM_WS_GATE
+ * regions hold next's inputs.  Decode calls (tokens == 1) ignore next and
+ * input_normed.  phase_events as above (with input_normed the norm+gate
+ * phase is empty).  No counterpart in the reference: it saves one kernel and
+ * one read of the hidden rows per layer and chunk. */
+int lm_moe_layer_forward_chain(const lm_moe_layer *layer,
+                               const lm_moe_layer *next, int input_normed,
+                               void *h, int64_t tokens, int64_t hidden,
+                               int64_t inter, int64_t experts, int64_t top_k,
+                               float eps, void *workspace,
+                               int64_t workspace_bytes, int32_t *ids_out,
+                               void *weights_out, void *const *phase_events,
+                               void *stream);
+
 /* lm_moe_layer_forward without a workspace argument: the call's workspace
  * is a device array inside the library (one per device, about 7.3 MB, held
  * until the process ends), so the call allocates nothing and takes no

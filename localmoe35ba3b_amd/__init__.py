@@ -8,4 +8,4 @@ include/localmoe35ba3b.h.
 from . import _lib  # noqa: F401
 
 __all__ = ['operators', 'runtime', 'convert', 'router']
-__version__ = '0.2.0'
+__version__ = '0.3.0'

@@ -55,6 +55,8 @@ SIGNATURES = {
     'lm_moe_workspace_init': (I32, [P, I64, P]),
     'lm_moe_workspace_region': (I32, [I64, I32, P, P]),
     'lm_moe_layer_forward': (I32, [P, P, I64, I64, I64, I64, I64, F32, P, I64, P, P, P, P]),
+    'lm_moe_layer_forward_chain': (I32, [P, P, I32, P, I64, I64, I64, I64, I64, F32, P, I64, P, P,
+                                         P, P]),
     'lm_moe_static_max_tokens': (I64, []),
     'lm_moe_static_init': (I32, []),
     'lm_moe_layer_forward_static': (I32, [P, P, I64, I64, I64, I64, I64, F32, P, P, P, P]),

@@ -22,7 +22,7 @@ int check_launch(const char *what) {
 
 }  // namespace lm
 
-extern "C" const char *lm_version(void) { return "localmoe35ba3b-amd 0.2 gfx950"; }
+extern "C" const char *lm_version(void) { return "localmoe35ba3b-amd 0.3 gfx950"; }
 
 extern "C" const char *lm_last_error(void) { return lm::g_last_error.c_str(); }
 

@@ -639,46 +639,36 @@ __global__ __launch_bounds__(256) void decode_down_kernel(int *p_sel, uint16_t *
 // token (workgroups < T) and |w_e| of each router row (workgroups < kE).
 // Leading pointer arguments: preloaded into SGPRs at launch, as in the decode
 // kernels.
-__global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, const uint16_t *p_router_w,
-                                                                const uint16_t *p_gate_w,
-                                                                const float *p_norm_w, int T,
-                                                                LayerArgs a) {
-  a.h = p_h;
-  a.router_w = p_router_w;
-  a.gate_w = p_gate_w;
-  a.norm_w = p_norm_w;
-  __shared__ float xf[kH];
-  __shared__ float red[4];
-  __shared__ float red2[4];
-  __shared__ double dred[4];
-  const int tok = blockIdx.x;
+//
+// The norm |w_e| of router row e (thread t holds its values 8 t .. 8 t + 7 in
+// wv), for the prefill router's error bound; red2 is reused.
+__device__ __forceinline__ void router_row_norm(u32x4 wv, float *nw_out, float *red2) {
+  const int t = threadIdx.x;
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float lo = bf16_bits_to_f32(wv[j] & 0xFFFFu), hi = bf16_bits_to_f32(wv[j] >> 16);
+    ss += lo * lo + hi * hi;
+  }
+  ss = wave_sum_f32(ss);
+  __syncthreads();  // red2 is free again
+  if ((t & 63) == 0) red2[t >> 6] = ss;
+  __syncthreads();
+  if (t == 0) *nw_out = sqrtf((red2[0] + red2[1]) + (red2[2] + red2[3]));
+}
+
+// The prefill norm work of token `tok` for the layer whose norm and gate
+// weights `a` holds (nwv, gv: thread t's norm weights and gate values
+// 8 t .. 8 t + 7): RMSNorm of the row (thread t holds its bf16 values
+// 8 t .. 8 t + 7 in raw) into xn, the row's Euclidean norm nx, the
+// shared-gate logit gl (fp64 dot) and, when a.xh is set, the fp16 copy of the
+// row for the gate_up GEMM on fp16 tiles with its power of two xk.
+__device__ __forceinline__ void prefill_norm_token(u32x4 raw, const NormW &nwv, u32x4 gv,
+                                                   const LayerArgs &a, int tok, float *xf,
+                                                   float *red, float *red2, double *dred) {
   const int t = threadIdx.x;
   constexpr int PER = kH / 256;
-  // Both weight rows are requested at entry, ahead of the token's row, so
-  // their latency overlaps the RMSNorm; the router-row norm (blocks < E) is
-  // finished after the token's work, which it must not delay.
-  const u32x4 wv = tok < kE ? ldg16(a.router_w + (int64_t)tok * kH + t * PER)
-                            : u32x4{0u, 0u, 0u, 0u};
-  const u32x4 gv = ldg16(a.gate_w + t * PER);
-  const NormW nwv = load_norm_w(a.norm_w);
-  auto router_row_norm = [&]() {
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float lo = bf16_bits_to_f32(wv[j] & 0xFFFFu), hi = bf16_bits_to_f32(wv[j] >> 16);
-      ss += lo * lo + hi * hi;
-    }
-    ss = wave_sum_f32(ss);
-    __syncthreads();  // red2 is free again
-    if ((t & 63) == 0) red2[t >> 6] = ss;
-    __syncthreads();
-    if (t == 0) a.nw[tok] = sqrtf((red2[0] + red2[1]) + (red2[2] + red2[3]));
-  };
-  if (tok >= T) {
-    if (tok < kE) router_row_norm();
-    return;
-  }
-  norm_row_to_lds(ldg16(a.h + (int64_t)tok * kH + t * PER), nwv, a.eps, xf, red);
+  norm_row_to_lds(raw, nwv, a.eps, xf, red);
   {
     float ss = 0.0f;
 #pragma unroll
@@ -725,7 +715,37 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, c
     *reinterpret_cast<u32x4 *>(a.xh + (int64_t)tok * kH + t * PER) = hp;
     if (t == 0) a.xk[tok] = k;
   }
-  if (tok < kE) router_row_norm();
+}
+
+__global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, const uint16_t *p_router_w,
+                                                                const uint16_t *p_gate_w,
+                                                                const float *p_norm_w, int T,
+                                                                LayerArgs a) {
+  a.h = p_h;
+  a.router_w = p_router_w;
+  a.gate_w = p_gate_w;
+  a.norm_w = p_norm_w;
+  __shared__ float xf[kH];
+  __shared__ float red[4];
+  __shared__ float red2[4];
+  __shared__ double dred[4];
+  const int tok = blockIdx.x;
+  const int t = threadIdx.x;
+  constexpr int PER = kH / 256;
+  // Both weight rows are requested at entry, ahead of the token's row, so
+  // their latency overlaps the RMSNorm; the router-row norm (blocks < E) is
+  // finished after the token's work, which it must not delay.
+  const u32x4 wv = tok < kE ? ldg16(a.router_w + (int64_t)tok * kH + t * PER)
+                            : u32x4{0u, 0u, 0u, 0u};
+  const u32x4 gv = ldg16(a.gate_w + t * PER);
+  const NormW nwv = load_norm_w(a.norm_w);
+  if (tok >= T) {
+    if (tok < kE) router_row_norm(wv, a.nw + tok, red2);
+    return;
+  }
+  prefill_norm_token(ldg16(a.h + (int64_t)tok * kH + t * PER), nwv, gv, a, tok, xf, red, red2,
+                     dred);
+  if (tok < kE) router_row_norm(wv, a.nw + tok, red2);
 }
 
 // Approximate router logits of the prefill tokens: bf16 MFMA with fp32
@@ -1166,15 +1186,46 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
   }
 }
 
+// The next layer of a chained prefill call: its weights for the norm work
+// that the combine does on the rows it has just written.
+struct NextLayer {
+  const uint16_t *router_w;
+  const uint16_t *gate_w;
+  const float *norm_w;
+  uint16_t *xh;  // the fp16 row copy, when the next gate_up runs on fp16 tiles
+};
+
 // Per token: routed combine in ascending expert order, gated shared add,
-// residual add (in place on h).  256 threads x 8 columns.
+// residual add (in place on h).  256 threads x 8 columns.  With NEXT the
+// same workgroup then does the next layer's norm work on the new row
+// (prefill_norm_token, the norm kernel's code and order, so the next layer
+// sees the same normalized rows, gate logits and fp16 copies as from its own
+// norm kernel) and workgroups < E the norms of the next router's rows; the
+// grid is then max(T, E) workgroups.
+template <bool NEXT>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(int64_t *p_ids, const int *rpos,
                                                               uint16_t *p_wts, const uint16_t *vbuf,
-                                                              int64_t R, LayerArgs a) {
+                                                              int64_t R, int T, LayerArgs a,
+                                                              NextLayer nx) {
   a.ids = p_ids;
   a.wts = p_wts;
   const int tok = blockIdx.x;
   const int c = threadIdx.x * 8;
+  __shared__ float xf[NEXT ? kH : 1];
+  __shared__ float red[4], red2[4];
+  __shared__ double dred[4];
+  // the next layer's weights, requested first (their latency overlaps the combine)
+  u32x4 wv{0u, 0u, 0u, 0u}, gv{0u, 0u, 0u, 0u};
+  NormW nwv{};
+  if constexpr (NEXT) {
+    if (tok < kE) wv = ldg16(nx.router_w + (int64_t)tok * kH + c);
+    gv = ldg16(nx.gate_w + c);
+    nwv = load_norm_w(nx.norm_w);
+    if (tok >= T) {
+      router_row_norm(wv, a.nw + tok, red2);
+      return;
+    }
+  }
   int e[kTopK], p[kTopK];
   float w[kTopK];
 #pragma unroll
@@ -1224,6 +1275,16 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(int64_t *p_ids, co
     outv[j] = BF16::pack2(o0, o1);
   }
   *reinterpret_cast<u32x4 *>(hp) = outv;
+  if constexpr (NEXT) {
+    // every thread has read this layer's gate logit (sig) before the
+    // barriers inside, after which thread 0 overwrites it with the next one
+    LayerArgs b = a;
+    b.norm_w = nx.norm_w;
+    b.gate_w = nx.gate_w;
+    b.xh = nx.xh;
+    prefill_norm_token(outv, nwv, gv, b, tok, xf, red, red2, dred);
+    if (tok < kE) router_row_norm(wv, a.nw + tok, red2);
+  }
 }
 
 __global__ void export_routing_kernel(const int64_t *ids, const uint16_t *wts, int32_t *ids_out,
@@ -1347,15 +1408,8 @@ int device_scratch(int dev, bool capturing, void **ptr) {
 }
 }  // namespace
 
-extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t tokens,
-                                    int64_t hidden, int64_t inter, int64_t experts, int64_t top_k,
-                                    float eps, void *workspace, int64_t workspace_bytes,
-                                    int32_t *ids_out, void *weights_out,
-                                    void *const *phase_events, void *stream) {
-  LM_REQUIRE(hidden == kH && inter == kI && experts == kE && top_k == kTopK, LM_EINVAL,
-             "fused MoE layer supports hidden 2048, intermediate 512, 256 experts, top-8");
-  LM_REQUIRE(tokens >= 1 && tokens <= 65536, LM_EINVAL, "invalid token count");
-  LM_REQUIRE(layer && h && workspace, LM_EINVAL, "null pointer");
+namespace {
+int check_layer(const lm_moe_layer *layer) {
   LM_REQUIRE(layer->struct_size == (int64_t)sizeof(lm_moe_layer), LM_EINVAL,
              "lm_moe_layer.struct_size differs from this library's sizeof(lm_moe_layer): "
              "set it, or rebuild the caller against this header");
@@ -1365,6 +1419,26 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   LM_REQUIRE(layer->gu_q_tiles_format == LM_TILES_PLAIN ||
                  layer->gu_q_tiles_format == LM_TILES_F16,
              LM_EINVAL, "unknown gu_q_tiles_format");
+  return LM_OK;
+}
+
+// The fused layer.  For prefill calls (tokens > 1): with `next`, the combine
+// also leaves next's normalized inputs for the same rows in the workspace;
+// with input_normed, the workspace already holds this layer's (a chained
+// call before it) and the norm kernel is not launched.  Decode calls ignore
+// both: their router kernel normalizes the row itself.
+int layer_forward(const lm_moe_layer *layer, const lm_moe_layer *next, bool input_normed,
+                  void *h, int64_t tokens, int64_t hidden, int64_t inter, int64_t experts,
+                  int64_t top_k, float eps, void *workspace, int64_t workspace_bytes,
+                  int32_t *ids_out, void *weights_out, void *const *phase_events, void *stream) {
+  LM_REQUIRE(hidden == kH && inter == kI && experts == kE && top_k == kTopK, LM_EINVAL,
+             "fused MoE layer supports hidden 2048, intermediate 512, 256 experts, top-8");
+  LM_REQUIRE(tokens >= 1 && tokens <= 65536, LM_EINVAL, "invalid token count");
+  LM_REQUIRE(layer && h && workspace, LM_EINVAL, "null pointer");
+  if (int rc = check_layer(layer)) return rc;
+  if (next) {
+    if (int rc = check_layer(next)) return rc;
+  }
   const WsLayout w = layout(tokens);
   LM_REQUIRE(workspace_bytes >= w.total, LM_ENOMEM, "workspace too small for this token count");
   unsigned char *ws = static_cast<unsigned char *>(workspace);
@@ -1439,9 +1513,11 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
   int *rpos = reinterpret_cast<int *>(ws + w.rpos);
   uint16_t *vbuf = a.vbuf;
   if (int rc = mark(0)) return rc;
-  prefill_norm_gate_kernel<<<(unsigned)(T > kE ? T : kE), 256, 0, st>>>(a.h, a.router_w, a.gate_w,
-                                                                    a.norm_w, (int)T, a);
-  if (int rc = check_launch("prefill_norm_gate_kernel")) return rc;
+  if (!input_normed) {
+    prefill_norm_gate_kernel<<<(unsigned)(T > kE ? T : kE), 256, 0, st>>>(
+        a.h, a.router_w, a.gate_w, a.norm_w, (int)T, a);
+    if (int rc = check_launch("prefill_norm_gate_kernel")) return rc;
+  }
   if (int rc = mark(1)) return rc;
   router_approx_kernel<<<dim3(cdiv(T, kRaTok), kE / kRaExp), 256, 0, st>>>(a.xn, a.router_w,
                                                                           a.logits, (int)T, a);
@@ -1471,7 +1547,17 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
                       kH,      kI,      false, false,  LM_BF16, layer->dn_q_tiles};
   if (int rc = routed_gemm(dn, st)) return rc;
   if (int rc = mark(6)) return rc;
-  prefill_combine_kernel<<<(unsigned)T, 256, 0, st>>>(a.ids, rpos, a.wts, vbuf, R, a);
+  if (next) {
+    const bool next_f16 = next->gu_q_tiles != nullptr && next->gu_q_tiles_format == LM_TILES_F16;
+    const NextLayer nl{static_cast<const uint16_t *>(next->router_w),
+                       static_cast<const uint16_t *>(next->shared_gate_w), next->norm_w,
+                       next_f16 ? reinterpret_cast<uint16_t *>(ws + w.xh) : nullptr};
+    prefill_combine_kernel<true><<<(unsigned)(T > kE ? T : kE), 256, 0, st>>>(
+        a.ids, rpos, a.wts, vbuf, R, (int)T, a, nl);
+  } else {
+    prefill_combine_kernel<false><<<(unsigned)T, 256, 0, st>>>(a.ids, rpos, a.wts, vbuf, R, (int)T,
+                                                              a, NextLayer{});
+  }
   if (int rc = check_launch("prefill_combine_kernel")) return rc;
   if (int rc = mark(7)) return rc;
   if (ids_out || weights_out) {
@@ -1479,6 +1565,28 @@ extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t 
     return check_launch("export_routing_kernel");
   }
   return LM_OK;
+}
+}  // namespace
+
+extern "C" int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t tokens,
+                                    int64_t hidden, int64_t inter, int64_t experts, int64_t top_k,
+                                    float eps, void *workspace, int64_t workspace_bytes,
+                                    int32_t *ids_out, void *weights_out,
+                                    void *const *phase_events, void *stream) {
+  return layer_forward(layer, nullptr, false, h, tokens, hidden, inter, experts, top_k, eps,
+                       workspace, workspace_bytes, ids_out, weights_out, phase_events, stream);
+}
+
+extern "C" int lm_moe_layer_forward_chain(const lm_moe_layer *layer, const lm_moe_layer *next,
+                                          int input_normed, void *h, int64_t tokens,
+                                          int64_t hidden, int64_t inter, int64_t experts,
+                                          int64_t top_k, float eps, void *workspace,
+                                          int64_t workspace_bytes, int32_t *ids_out,
+                                          void *weights_out, void *const *phase_events,
+                                          void *stream) {
+  return layer_forward(layer, next, input_normed != 0, h, tokens, hidden, inter, experts, top_k,
+                       eps, workspace, workspace_bytes, ids_out, weights_out, phase_events,
+                       stream);
 }
 
 extern "C" int64_t lm_moe_static_max_tokens(void) { return kScratchMaxTokens; }

@@ -169,9 +169,16 @@ class MoEStack:
         _lib.call('lm_moe_workspace_init', ws.data_ptr(), ws.numel(), _lib.stream(self.device))
         return ws
 
-    def layer_forward(self, h, l, ids_out=None, weights_out=None, events=None, workspace=None):
+    def layer_forward(self, h, l, ids_out=None, weights_out=None, events=None, workspace=None,
+                      next_layer=None, input_normed=False):
         """h bf16 [T, H] updated in place: h = h + block(rmsnorm(h)).  Chunks
-        in flight at the same time need workspaces of their own."""
+        in flight at the same time need workspaces of their own.
+
+        Chained calls (lm_moe_layer_forward_chain): with next_layer, the call
+        also leaves layer next_layer's normalized inputs for these rows in the
+        workspace; the following call for next_layer, on the same rows and
+        workspace, passes input_normed=True and skips its norm kernel.  The
+        results are bit-identical to unchained calls."""
         if h.dtype != torch.bfloat16 or not h.is_contiguous() or h.shape[-1] != self.H:
             raise ValueError('expected contiguous bf16 [tokens, 2048] hidden states')
         tokens = h.shape[0]
@@ -182,9 +189,16 @@ class MoEStack:
         if events is not None:
             ev = (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
         ws = self.workspace if workspace is None else workspace
-        _lib.call('lm_moe_layer_forward', ctypes.byref(self._structs[l]), h.data_ptr(), tokens,
-                  self.H, self.I, self.E, self.K, EPS, ws.data_ptr(), ws.numel(),
-                  _lib.ptr(ids_out), _lib.ptr(weights_out), ev, _lib.stream(h.device))
+        if next_layer is None and not input_normed:
+            _lib.call('lm_moe_layer_forward', ctypes.byref(self._structs[l]), h.data_ptr(), tokens,
+                      self.H, self.I, self.E, self.K, EPS, ws.data_ptr(), ws.numel(),
+                      _lib.ptr(ids_out), _lib.ptr(weights_out), ev, _lib.stream(h.device))
+            return h
+        nxt = None if next_layer is None else ctypes.byref(self._structs[next_layer])
+        _lib.call('lm_moe_layer_forward_chain', ctypes.byref(self._structs[l]), nxt,
+                  int(bool(input_normed)), h.data_ptr(), tokens, self.H, self.I, self.E, self.K,
+                  EPS, ws.data_ptr(), ws.numel(), _lib.ptr(ids_out), _lib.ptr(weights_out), ev,
+                  _lib.stream(h.device))
         return h
 
     _REGION_TYPES = {'normed': (torch.bfloat16, 'H'), 'gate': (torch.float32, None),
@@ -232,9 +246,15 @@ class MoEStack:
                       _lib.ptr(ids_out), _lib.ptr(weights_out), None, _lib.stream(h.device))
         return h
 
-    def forward(self, h, layers=None):
-        for l in range(self.L if layers is None else layers):
-            self.layer_forward(h, l)
+    def forward(self, h, layers=None, workspace=None, chain=True):
+        """All (or the first `layers`) layers over h in place, one workspace;
+        with chain, each layer's combine prepares the next layer's normalized
+        rows (layer_forward's next_layer / input_normed)."""
+        n = self.L if layers is None else layers
+        for l in range(n):
+            self.layer_forward(h, l, workspace=workspace,
+                               next_layer=l + 1 if chain and l + 1 < n else None,
+                               input_normed=chain and l > 0)
         return h
 
     def prefill(self, x, chunk=2048, overlap=True):
@@ -281,13 +301,17 @@ class MoEStack:
         streams, spaces = (cur, self._side), (self.workspace, self._side_ws)
         self._side.wait_stream(cur)
         done = [[torch.cuda.Event() for _ in range(self.L)] for _ in starts]
+        # chained layers need a workspace per chunk (two chunks, two workspaces)
+        chain = len(starts) == 2
         for l in range(self.L):
             for c, c0 in enumerate(starts):
                 st = streams[c % 2]
                 with torch.cuda.stream(st):
                     if c and l:
                         st.wait_event(done[c - 1][l - 1])
-                    self.layer_forward(h[c0:c0 + chunk], l, workspace=spaces[c % 2])
+                    self.layer_forward(h[c0:c0 + chunk], l, workspace=spaces[c % 2],
+                                       next_layer=l + 1 if chain and l + 1 < self.L else None,
+                                       input_normed=chain and l > 0)
                     done[c][l].record(st)
         cur.wait_stream(self._side)
         self._done_events = done  # kept alive until the next call

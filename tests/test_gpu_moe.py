@@ -329,6 +329,30 @@ def test_prefill_extreme_inputs(dev, fmt, monkeypatch):
     assert_close(npf(out), model, BF16_TOL, 'extreme inputs, fp16 gate_up vs its model')
 
 
+@pytest.mark.parametrize('fmt', [0, 1])
+@pytest.mark.parametrize('tokens', [1, 100, 300])
+def test_chained_layers_bit_identical(dev, fmt, tokens):
+    """Chained layer calls (lm_moe_layer_forward_chain: each combine does the
+    next layer's norm work, the next call skips its norm kernel) give the
+    unchained calls' results bit for bit: random RMSNorm weights, both gate_up
+    tile formats (the fp16 row copy is made for the next layer), fewer tokens
+    than experts (workgroups past the tokens only take router-row norms) and a
+    decode call, which ignores the chain.  The overlapped prefill chains its
+    two chunks' layers too."""
+    st = SyntheticMoEStack(layers=3, seed=31, device=dev, max_tokens=512, norm=True,
+                           gate_up_format=fmt)
+    g = torch.Generator(device=dev)
+    g.manual_seed(32)
+    st.norm_w.copy_(torch.randn(st.norm_w.shape, generator=g, device=dev) * 0.3)
+    h = inputs(tokens, 33, dev)
+    plain = st.forward(h.clone(), chain=False)
+    chained = st.forward(h.clone(), chain=True)
+    assert torch.equal(plain, chained)
+    if tokens > 1:
+        two = st.prefill(h, chunk=(tokens + 1) // 2, overlap=True)  # two chained chunks
+        assert torch.equal(two, plain)
+
+
 def test_tile_copy_stale_weights_refused(dev):
     """Writing gu_q or dn_q in place after build_prefill_tiles leaves the
     prefill tile copies stale: the stack refuses to run until they are
