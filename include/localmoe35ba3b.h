@@ -371,8 +371,10 @@ int lm_moe_layer_forward(const lm_moe_layer *layer, void *h, int64_t tokens,
  * order as next's own norm kernel, so the results are bit-identical to
  * unchained calls.  The next call, on the same rows, workspace, stream and
  * eps with layer == this call's next, passes input_normed = 1 and skips its
- * norm kernel.  After a call with next, the LM_WS_NORMED and LM_WS_GATE
- * regions hold next's inputs.  Decode calls (tokens == 1) ignore next and
+ * norm kernel; the library remembers, per workspace, which layer, token
+ * count and eps the last prefill call prepared, and refuses input_normed = 1
+ * otherwise (LM_EINVAL, before any launch).  After a call with next, the
+ * LM_WS_NORMED and LM_WS_GATE regions hold next's inputs.  Decode calls (tokens == 1) ignore next and
  * input_normed.  phase_events as above (with input_normed the norm+gate
  * phase is empty).  No counterpart in the reference: it saves one kernel and
  * one read of the hidden rows per layer and chunk. */

@@ -20,6 +20,7 @@
 // grouped W8A16 down GEMM, and a per-token combine.
 #include <algorithm>
 #include <mutex>
+#include <unordered_map>
 
 #include "gemv_core.hpp"
 #include "internal.hpp"
@@ -1409,6 +1410,18 @@ int device_scratch(int dev, bool capturing, void **ptr) {
 }  // namespace
 
 namespace {
+// What the last prefill call on each workspace left there for a chained
+// successor: the layer whose normalized inputs it wrote, for how many rows
+// and with which eps (none after an unchained call).  Host-side calls are in
+// stream order per workspace, also while a HIP graph is captured.
+struct ChainState {
+  const lm_moe_layer *next;
+  int64_t tokens;
+  float eps;
+};
+std::mutex g_chain_mutex;
+std::unordered_map<const void *, ChainState> g_chain;
+
 int check_layer(const lm_moe_layer *layer) {
   LM_REQUIRE(layer->struct_size == (int64_t)sizeof(lm_moe_layer), LM_EINVAL,
              "lm_moe_layer.struct_size differs from this library's sizeof(lm_moe_layer): "
@@ -1441,6 +1454,21 @@ int layer_forward(const lm_moe_layer *layer, const lm_moe_layer *next, bool inpu
   }
   const WsLayout w = layout(tokens);
   LM_REQUIRE(workspace_bytes >= w.total, LM_ENOMEM, "workspace too small for this token count");
+  if (tokens > 1) {  // decode calls neither use nor leave normalized inputs
+    std::lock_guard<std::mutex> lock(g_chain_mutex);
+    if (input_normed) {
+      const auto it = g_chain.find(workspace);
+      LM_REQUIRE(it != g_chain.end() && it->second.next == layer && it->second.tokens == tokens &&
+                     it->second.eps == eps,
+                 LM_EINVAL,
+                 "input_normed: the previous call on this workspace did not chain into this "
+                 "layer with the same token count and eps");
+    }
+    if (next)
+      g_chain[workspace] = ChainState{next, tokens, eps};
+    else
+      g_chain.erase(workspace);
+  }
   unsigned char *ws = static_cast<unsigned char *>(workspace);
   LayerArgs a{};
   a.router_w = static_cast<const uint16_t *>(layer->router_w);

@@ -121,6 +121,20 @@ def test_moe_layer_bounds_rejected_before_launch():
     assert b'gu_q_tiles_format' in lib.lm_last_error()
 
 
+def test_chained_input_normed_refused_without_chain():
+    """lm_moe_layer_forward_chain refuses input_normed = 1 unless the previous
+    call on the same workspace chained into this layer (same tokens and eps),
+    before any launch."""
+    lib = _lib.lib()
+    fake = 512
+    layer = _lib.MoeLayer(*([fake] * 8), 0, 0, 0, 0)
+    ws = lib.lm_moe_workspace_bytes(64, 2048, 512, 256, 8)
+    rc = lib.lm_moe_layer_forward_chain(ctypes.byref(layer), None, 1, fake, 16, 2048, 512, 256, 8,
+                                        1e-6, fake + 4096, ws, None, None, None, None)
+    assert rc == _lib.LM_EINVAL
+    assert b'input_normed' in lib.lm_last_error()
+
+
 def test_workspace_regions():
     """Every region lies inside the workspace of its token count; the
     decode-only regions (W8A8 intermediates of the one-token path) and the

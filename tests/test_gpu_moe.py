@@ -348,6 +348,14 @@ def test_chained_layers_bit_identical(dev, fmt, tokens):
     plain = st.forward(h.clone(), chain=False)
     chained = st.forward(h.clone(), chain=True)
     assert torch.equal(plain, chained)
+    if tokens > 1:  # input_normed only right after a call that chained into the layer
+        with pytest.raises(Exception, match='input_normed'):
+            st.layer_forward(h.clone(), 1, input_normed=True)  # the last call did not chain
+        st.layer_forward(h.clone(), 0, next_layer=1)
+        with pytest.raises(Exception, match='input_normed'):
+            st.layer_forward(h.clone(), 2, input_normed=True)  # it chained into layer 1
+        with pytest.raises(Exception, match='input_normed'):
+            st.layer_forward(h[:-1].clone(), 1, input_normed=True)  # other token count
     if tokens > 1:
         two = st.prefill(h, chunk=(tokens + 1) // 2, overlap=True)  # two chained chunks
         assert torch.equal(two, plain)
