@@ -1352,9 +1352,28 @@ extern "C" int lm_moe_workspace_region(int64_t tokens, int region, int64_t *offs
   return LM_OK;
 }
 
+namespace {
+// What the last prefill call on each workspace left there for a chained
+// successor: the layer whose normalized inputs it wrote, for how many rows
+// and with which eps (none after an unchained call).  Host-side calls are in
+// stream order per workspace, also while a HIP graph is captured.
+struct ChainState {
+  const lm_moe_layer *next;
+  int64_t tokens;
+  float eps;
+};
+std::mutex g_chain_mutex;
+std::unordered_map<const void *, ChainState> g_chain;
+
+}  // namespace
+
 extern "C" int lm_moe_workspace_init(void *workspace, int64_t bytes, void *stream) {
   LM_REQUIRE(workspace && bytes >= 256 && bytes % 4 == 0, LM_EINVAL,
              "workspace must be at least 256 bytes and a multiple of 4");
+  {  // a (re)initialized workspace holds no chained layer's inputs
+    std::lock_guard<std::mutex> lock(g_chain_mutex);
+    g_chain.erase(workspace);
+  }
   const int64_t blocks = std::min<int64_t>(cdiv(bytes >> 2, 256), 4096);
   fill_zero_kernel<<<(unsigned)blocks, 256, 0, as_stream(stream)>>>(
       static_cast<uint32_t *>(workspace), bytes);
@@ -1410,18 +1429,6 @@ int device_scratch(int dev, bool capturing, void **ptr) {
 }  // namespace
 
 namespace {
-// What the last prefill call on each workspace left there for a chained
-// successor: the layer whose normalized inputs it wrote, for how many rows
-// and with which eps (none after an unchained call).  Host-side calls are in
-// stream order per workspace, also while a HIP graph is captured.
-struct ChainState {
-  const lm_moe_layer *next;
-  int64_t tokens;
-  float eps;
-};
-std::mutex g_chain_mutex;
-std::unordered_map<const void *, ChainState> g_chain;
-
 int check_layer(const lm_moe_layer *layer) {
   LM_REQUIRE(layer->struct_size == (int64_t)sizeof(lm_moe_layer), LM_EINVAL,
              "lm_moe_layer.struct_size differs from this library's sizeof(lm_moe_layer): "
