@@ -499,10 +499,13 @@ def main():
         pgraph.replay()
 
     def prefill_kernel_probe():
+        # chained like the timed graph: after layer 0 the norm phase is empty
+        # and each combine does the next layer's norm work
         pprobe.copy_(x[:CHUNK])
         torch.cuda._sleep(3 * spin_cycles)
         for l in range(L):
-            stack.layer_forward(pprobe, l, events=pf_events[l])
+            stack.layer_forward(pprobe, l, events=pf_events[l],
+                                next_layer=l + 1 if l + 1 < L else None, input_normed=l > 0)
 
     def decode():
         for i in range(DECODE_TOKENS):
