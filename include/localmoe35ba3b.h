@@ -321,6 +321,14 @@ int lm_moe_workspace_init(void *workspace, int64_t bytes, void *stream);
  *   LM_WS_DOWN        bf16  [R + tokens, H]  down rows (routed, then shared)
  * of prefill calls (tokens > 1) only:
  *   LM_WS_ROUTE_ROWS  int32 [tokens, top_k]  expert-sorted row of each route
+ *   LM_WS_ROUTER_APPROX fp32 [tokens, experts] approximate router logits A
+ *                                            (bf16 MFMA, fp32 sums, before
+ *                                            the bias); the selection takes
+ *                                            |A - x.w_e| <= 2^-17 |x| |w_e|
+ *   LM_WS_ROW_NORMS   fp32  [tokens]         |x| of each normalized row
+ *   LM_WS_ROUTER_NORMS fp32 [experts]        |w_e| of each router row
+ *   (after a chained call, LM_WS_NORMED, LM_WS_ROW_NORMS and
+ *   LM_WS_ROUTER_NORMS hold the next layer's inputs instead)
  * of decode calls (tokens == 1) only, whose routed rows in LM_WS_HIDDEN and
  * LM_WS_DOWN are in combine order (ascending expert id, slot s = row s):
  *   LM_WS_ACT_Q       int8  [H]              w8a8.quantize of the normed row
@@ -345,6 +353,9 @@ int lm_moe_workspace_init(void *workspace, int64_t bytes, void *stream);
 #define LM_WS_SLOT_WEIGHTS 10
 #define LM_WS_GATE_UP_ACC 11
 #define LM_WS_DOWN_ACC 12
+#define LM_WS_ROUTER_APPROX 13
+#define LM_WS_ROW_NORMS 14
+#define LM_WS_ROUTER_NORMS 15
 int lm_moe_workspace_region(int64_t tokens, int region, int64_t *offset,
                             int64_t *bytes);
 

@@ -18,7 +18,8 @@ LM_TILES_PLAIN, LM_TILES_F16 = 0, 1
 # fused-layer workspace regions (lm_moe_workspace_region)
 WS_REGIONS = {'normed': 0, 'gate': 1, 'ids': 2, 'weights': 3, 'route_rows': 4, 'hidden': 5,
               'down': 6, 'act_q': 7, 'act_scales': 8, 'slot_ids': 9, 'slot_weights': 10,
-              'gate_up_acc': 11, 'down_acc': 12}
+              'gate_up_acc': 11, 'down_acc': 12, 'router_approx': 13, 'row_norms': 14,
+              'router_norms': 15}
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64

@@ -28,7 +28,12 @@ COMMON = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}', '-ffp-contract
 # leading scalar arguments (up to 6) into SGPRs at launch; the decode kernels
 # take the pointers their first loads need as such arguments.  The compiler
 # emits a prologue that loads them normally for firmware without preloading.
-EXTRA = {'moe.hip': ['-mllvm', '-amdgpu-kernarg-preload-count=6']}
+# The VGPR form of the MFMA instructions: the prefill router adds each MFMA
+# result to an fp32 sum on the VALU, which reads VGPR results directly
+# instead of copying them out of AGPRs (the router is moe.hip's only MFMA
+# user).
+EXTRA = {'moe.hip': ['-mllvm', '-amdgpu-kernarg-preload-count=6',
+                     '-mllvm', '-amdgpu-mfma-vgpr-form=1']}
 
 
 def hipcc():

@@ -818,10 +818,21 @@ router_approx_kernel(uint16_t *p_xn, const uint16_t *p_router_w, float *p_logits
       for (int j = 0; j < 4; ++j)
         bv[j] = *reinterpret_cast<const u32x4 *>(my + (kRaTok + 16 * j + r) * PITCH + st * 64 +
                                                  q * 16);
+      // each MFMA sums its 32 products from zero; its result is added to
+      // the running fp32 sum, which bounds the roundings a product passes
+      // through by 31 + 15 + 3 (see topk_exact_wave)
+      // (all eight MFMAs issue before the first add reads a result)
+      f32x4 pr[2][4];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = BF16::mfma16x16x32(av[i], bv[j], acc[i][j]);
+        for (int j = 0; j < 4; ++j)
+          pr[i][j] = BF16::mfma16x16x32(av[i], bv[j], f32x4{0.f, 0.f, 0.f, 0.f});
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = acc[i][j] + pr[i][j];
     }
     wave_lds_sync();  // every lane's reads before the next segment is stored
   }
@@ -849,21 +860,29 @@ router_approx_kernel(uint16_t *p_xn, const uint16_t *p_router_w, float *p_logits
 
 // Exact top-8 of one prefill token (one wave) from the approximate logits.
 // An approximate logit A is the fp32 sum of the exactly representable
-// bf16 x bf16 products with at most kH + kH / 32 fp32 roundings, so
-// |A - S| <= (kH + kH / 32) 2^-23 sum_k |x_k w_ek| <= 2^-11 |x| |w_e| / 1.01
-// for the exact dot product S (Cauchy-Schwarz; the 1% absorbs the
-// rounding of the norms and of A -/+ eps).  Rounding to bf16 and adding the
-// bias are monotone, so the exact logit round_bf16(S) (+ bias) lies in
-// [round_bf16(A - eps), round_bf16(A + eps)] (+ bias).  With T8 the 8th largest
-// lower-bound key, an expert whose upper-bound key is below T8 is beaten by
-// 8 experts whatever its exact logit is; every other expert (a candidate,
-// typically 8 to 10) gets its exact logit from an fp64 dot product, the same
-// value router_logits computes.  The selection and softmax then run on
+// bf16 x bf16 products: each MFMA of router_approx_kernel sums 32 of them
+// from zero (at most 31 roundings in any order), its result joins the
+// wave's running sum of 16 MFMAs (15 roundings) and the four waves' sums
+// are added (3), so a product passes through at most 49 roundings and
+// |A - S| <= 49 2^-23 sum_k |x_k w_ek| <= 49 2^-23 |x| |w_e| <= 2^-17 |x| |w_e| / 1.3
+// for the exact dot product S (Cauchy-Schwarz; the 30% absorbs the second-
+// order terms, the fp64 error of the exact dot products and the rounding
+// of the norms and of eps).  Rounding to bf16 and adding the bias are
+// monotone, so the exact logit round_bf16(S) (+ bias) lies in
+// [lo, hi] = [round_bf16(A - eps), round_bf16(A + eps)] (+ bias).  With T8
+// the 8th largest lower-bound key, an expert whose upper-bound key is below
+// T8 is beaten by 8 experts whatever its exact logit is; every other expert
+// is a candidate.  A candidate with lo == hi has that exact logit already,
+// and so has round_bf16(A) (+ bias), which lies between them; only the
+// others (lo < hi: A within eps of a bf16 rounding boundary, a few percent
+// of the candidates) get their exact logit from an fp64 dot product, the
+// same value router_logits computes.  The selection and softmax then run on
 // exact logits for the candidates and rounded approximate ones elsewhere,
 // which can only enter the softmax denominator.
 template <class KT>
 __device__ void topk_exact_wave(const LayerArgs &a, int tok, int lane, unsigned long long *scratch,
-                                float *lv, int *cand, int64_t *ids_out, uint16_t *w_out) {
+                                float *lv, int *cand, int *amb, int64_t *ids_out,
+                                uint16_t *w_out) {
   using T = typename KT::T;
   u32x4 xv[4];  // the token's row, needed once the candidates are known
   {
@@ -881,7 +900,7 @@ __device__ void topk_exact_wave(const LayerArgs &a, int tok, int lane, unsigned 
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int e = lane * 4 + j;
-    const float eps = 0x1.0p-11f * 1.01f * (nx * NW[j]) + 1e-30f;
+    const float eps = 0x1.0p-17f * (nx * NW[j]) + 1e-30f;
     lo[j] = round_bf16(A[j] - eps);
     hi[j] = round_bf16(A[j] + eps);
     float ap = round_bf16(A[j]);
@@ -897,28 +916,36 @@ __device__ void topk_exact_wave(const LayerArgs &a, int tok, int lane, unsigned 
   }
   static_assert(kTopK == 8, "T8 is the 8th largest lower-bound key");
   const T t8 = kth8_key_wave<KT>(klo, lane);
-  // candidates, compacted into cand[0 .. n)
-  int n = 0;
+  // candidates, compacted into cand[0 .. n); the ones whose exact logit
+  // the bounds leave open (lo != hi, also when either is NaN) into
+  // amb[0 .. na)
+  int n = 0, na = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const bool c = khi[j] >= t8;
     const unsigned long long m = __ballot(c);
-    const uint32_t mlo = (uint32_t)m, mhi = (uint32_t)(m >> 32);
-    const int before = (int)__builtin_amdgcn_mbcnt_hi(mhi, __builtin_amdgcn_mbcnt_lo(mlo, 0u));
+    const int before = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
     if (c) cand[n + before] = lane * 4 + j;
     n += __popcll(m);
+    const bool o = c && !(lo[j] == hi[j]);
+    const unsigned long long mo = __ballot(o);
+    const int bo = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mo >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)mo, 0u));
+    if (o) amb[na + bo] = lane * 4 + j;
+    na += __popcll(mo);
   }
   wave_lds_sync();
-  // exact logits, CB candidates per batch, the next batch's rows requested
-  // before the current batch is reduced: lane holds x[k] and w[k] for
-  // k = 8 lane + 512 i + (0..7)
+  // exact logits of the open candidates, CB per batch, the next batch's
+  // rows requested before the current batch is reduced: lane holds x[k]
+  // and w[k] for k = 8 lane + 512 i + (0..7)
   constexpr int CB = 3;
   u32x4 wv[2][CB][4];
   int ec[2][CB];
   auto fetch = [&](int buf, int c0) {
 #pragma unroll
     for (int b = 0; b < CB; ++b) {
-      ec[buf][b] = cand[min(c0 + b, n - 1)];
+      ec[buf][b] = amb[min(c0 + b, na - 1)];
       const uint16_t *wr = a.router_w + (int64_t)ec[buf][b] * kH + lane * 8;
 #pragma unroll
       for (int i = 0; i < 4; ++i) wv[buf][b][i] = ldg16(wr + 512 * i);
@@ -942,19 +969,19 @@ __device__ void topk_exact_wave(const LayerArgs &a, int tok, int lane, unsigned 
 #pragma unroll
     for (int b = 0; b < CB; ++b) {
       const double sum = wave_sum_f64_dpp(acc[b]);
-      if (lane == 0 && c0 + b < n) {
+      if (lane == 0 && c0 + b < na) {
         float l = round_bf16((float)sum);
         if (a.router_bias) l = l + a.router_bias[ec[buf][b]];
         lv[ec[buf][b]] = l;
       }
     }
   };
-  fetch(0, 0);
-  for (int c0 = 0; c0 < n; c0 += 2 * CB) {
-    if (c0 + CB < n) fetch(1, c0 + CB);
+  if (na > 0) fetch(0, 0);
+  for (int c0 = 0; c0 < na; c0 += 2 * CB) {
+    if (c0 + CB < na) fetch(1, c0 + CB);
     reduce(0, c0);
-    if (c0 + 2 * CB < n) fetch(0, c0 + 2 * CB);
-    if (c0 + CB < n) reduce(1, c0 + CB);
+    if (c0 + 2 * CB < na) fetch(0, c0 + 2 * CB);
+    if (c0 + CB < na) reduce(1, c0 + CB);
   }
   wave_lds_sync();
   float v[4];
@@ -1028,6 +1055,7 @@ __global__ __launch_bounds__(kTopkTokens * 64) void prefill_topk_count_kernel(
   __shared__ unsigned long long scratch[kTopkTokens][kTopkScratch];
   __shared__ float lv[kTopkTokens][kE];
   __shared__ int cand[kTopkTokens][kE];
+  __shared__ int amb[kTopkTokens][kE];
   static_assert(kTopkTokens * 64 >= kE, "one thread per expert count");
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -1038,9 +1066,9 @@ __global__ __launch_bounds__(kTopkTokens * 64) void prefill_topk_count_kernel(
   int e = -1, rank = 0;
   if (tok < T) {  // wave-uniform
     if (a.router_bias)
-      topk_exact_wave<Key64>(a, tok, lane, scratch[w], lv[w], cand[w], sid[w], swt[w]);
+      topk_exact_wave<Key64>(a, tok, lane, scratch[w], lv[w], cand[w], amb[w], sid[w], swt[w]);
     else
-      topk_exact_wave<Key32>(a, tok, lane, scratch[w], lv[w], cand[w], sid[w], swt[w]);
+      topk_exact_wave<Key32>(a, tok, lane, scratch[w], lv[w], cand[w], amb[w], sid[w], swt[w]);
     wave_lds_sync();
     if (lane < kTopK) {
       e = (int)clamp_index(sid[w][lane], kE);
@@ -1329,6 +1357,18 @@ extern "C" int lm_moe_workspace_region(int64_t tokens, int region, int64_t *offs
     case LM_WS_ROUTE_ROWS:
       LM_REQUIRE(!decode, LM_EINVAL, "a decode call has no route rows");
       *offset = w.rpos; *bytes = R * 4; break;
+    case LM_WS_ROUTER_APPROX:
+    case LM_WS_ROW_NORMS:
+    case LM_WS_ROUTER_NORMS:
+      LM_REQUIRE(!decode, LM_EINVAL, "region written by prefill calls (tokens > 1) only");
+      if (region == LM_WS_ROUTER_APPROX) {
+        *offset = w.logits; *bytes = T * kE * 4;
+      } else if (region == LM_WS_ROW_NORMS) {
+        *offset = w.nx; *bytes = T * 4;
+      } else {
+        *offset = w.nw; *bytes = kE * 4;
+      }
+      break;
     case LM_WS_HIDDEN: *offset = w.hbuf; *bytes = (R + T) * kI * 2; break;
     case LM_WS_DOWN: *offset = w.vbuf; *bytes = (R + T) * kH * 2; break;
     case LM_WS_ACT_Q:

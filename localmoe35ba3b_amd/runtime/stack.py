@@ -207,15 +207,19 @@ class MoEStack:
                      'down': (torch.bfloat16, 'H'), 'act_q': (torch.int8, None),
                      'act_scales': (torch.float32, None), 'slot_ids': (torch.int32, None),
                      'slot_weights': (torch.float32, None),
-                     'gate_up_acc': (torch.float32, '2I'), 'down_acc': (torch.float32, 'H')}
+                     'gate_up_acc': (torch.float32, '2I'), 'down_acc': (torch.float32, 'H'),
+                     'router_approx': (torch.float32, 'E'), 'row_norms': (torch.float32, None),
+                     'router_norms': (torch.float32, None)}
 
     def workspace_view(self, region, tokens, workspace=None):
         """Typed view of one intermediate a call on `tokens` rows left in the
         workspace (lm_moe_workspace_region): 'normed', 'gate', 'ids',
-        'weights', 'hidden', 'down'; 'route_rows' of prefill calls; the W8A8
-        intermediates of decode calls 'act_q', 'act_scales', 'slot_ids',
-        'slot_weights', 'gate_up_acc', 'down_acc'.  Valid until the next call
-        that uses the same workspace."""
+        'weights', 'hidden', 'down'; of prefill calls 'route_rows' and the
+        approximate router logits with the norms of their error bound
+        'router_approx', 'row_norms', 'router_norms'; the W8A8 intermediates
+        of decode calls 'act_q', 'act_scales', 'slot_ids', 'slot_weights',
+        'gate_up_acc', 'down_acc'.  Valid until the next call that uses the
+        same workspace."""
         ws = self.workspace if workspace is None else workspace
         off, nbytes = ctypes.c_int64(), ctypes.c_int64()
         _lib.call('lm_moe_workspace_region', tokens, _lib.WS_REGIONS[region],
@@ -224,7 +228,8 @@ class MoEStack:
         raw = ws[off.value:off.value + nbytes.value].view(dtype)
         if inner is None:
             return raw
-        return raw.view(-1, {'H': self.H, 'I': self.I, 'K': self.K, '2I': 2 * self.I}[inner])
+        return raw.view(-1, {'H': self.H, 'I': self.I, 'K': self.K, '2I': 2 * self.I,
+                             'E': self.E}[inner])
 
     def layer_forward_static(self, h, l, ids_out=None, weights_out=None):
         """layer_forward through lm_moe_layer_forward_static: the workspace is

@@ -138,7 +138,8 @@ def test_chained_input_normed_refused_without_chain():
 def test_workspace_regions():
     """Every region lies inside the workspace of its token count; the
     decode-only regions (W8A8 intermediates of the one-token path) and the
-    prefill-only route rows are refused for the other kind of call."""
+    prefill-only ones (route rows, approximate router logits and their
+    norms) are refused for the other kind of call."""
     lib = _lib.lib()
     off, nb = ctypes.c_int64(), ctypes.c_int64()
     for tokens in (1, 2, 37, 2048):
@@ -146,8 +147,9 @@ def test_workspace_regions():
         spans = []
         for name, code in _lib.WS_REGIONS.items():
             rc = lib.lm_moe_workspace_region(tokens, code, ctypes.byref(off), ctypes.byref(nb))
-            decode_only = code >= 7
-            if (tokens == 1 and name == 'route_rows') or (tokens > 1 and decode_only):
+            decode_only = 7 <= code <= 12
+            prefill_only = name == 'route_rows' or code >= 13
+            if (tokens == 1 and prefill_only) or (tokens > 1 and decode_only):
                 assert rc == _lib.LM_EINVAL, (tokens, name)
                 continue
             assert rc == _lib.LM_OK, (tokens, name)
@@ -164,7 +166,12 @@ def test_workspace_regions():
     assert sizes == {'hidden': 9 * 512 * 2, 'down': 9 * 2048 * 2, 'act_q': 2048,
                      'act_scales': 16 * 4, 'slot_ids': 32, 'slot_weights': 32,
                      'gate_up_acc': 8 * 1024 * 4, 'down_acc': 8 * 2048 * 4}
-    assert lib.lm_moe_workspace_region(1, 13, ctypes.byref(off), ctypes.byref(nb)) == _lib.LM_EINVAL
+    for name, size in (('router_approx', 37 * 256 * 4), ('row_norms', 37 * 4),
+                       ('router_norms', 256 * 4)):
+        assert lib.lm_moe_workspace_region(37, _lib.WS_REGIONS[name], ctypes.byref(off),
+                                           ctypes.byref(nb)) == _lib.LM_OK
+        assert nb.value == size, name
+    assert lib.lm_moe_workspace_region(2, 16, ctypes.byref(off), ctypes.byref(nb)) == _lib.LM_EINVAL
 
 
 def test_status_maps_to_reference_exceptions():

@@ -472,6 +472,52 @@ def test_prefill_weights_vs_exact_router(dev, capsys):
     assert rate < 1e-2
 
 
+@pytest.mark.parametrize('mode', ['random', 'wide_range', 'aligned'])
+def test_router_approx_error_bound(dev, capsys, mode):
+    """The prefill selection rests on the error of the approximate router
+    logits A: each bf16 MFMA sums its 32 exact products from zero and the
+    results are added in fp32, so a product passes through at most 49
+    roundings and |A - S| <= 49 2^-23 sum_k |x_k w_ek| <= 2^-17 |x| |w_e|.
+    Checked on every (token, expert) pair against float64 dot products of
+    the same bf16 rows, for random rows, rows whose elements span 2^-40 ..
+    2^20 (products of every magnitude inside one MFMA) and rows along one
+    router row each (logits near |x| |w_e|, sums of same-sign products).
+    The norms the bound uses are checked against float64 norms."""
+    T = 512
+    st = SyntheticMoEStack(layers=1, seed=61, device=dev, max_tokens=T)
+    g = torch.Generator()
+    g.manual_seed(62)
+    if mode == 'random':
+        h = torch.randn(T, 2048, generator=g)
+    elif mode == 'wide_range':
+        h = torch.randn(T, 2048, generator=g) * torch.exp2(
+            torch.randint(-40, 21, (T, 2048), generator=g).float())
+    else:
+        pick = torch.randint(0, 256, (T,), generator=g)
+        sign = torch.where(torch.rand(T, 1, generator=g) < 0.5, -1.0, 1.0)
+        h = st.router_w[0].float().cpu()[pick] * sign * 50 + \
+            torch.randn(T, 2048, generator=g) * 0.01
+    h = h.to(torch.bfloat16).to(dev)
+    run_layer(st, h)
+    A = st.workspace_view('router_approx', T).double().cpu().numpy()
+    nx = st.workspace_view('row_norms', T).double().cpu().numpy()
+    nw = st.workspace_view('router_norms', T).double().cpu().numpy()
+    xn = st.workspace_view('normed', T).double().cpu().numpy()
+    W = st.router_w[0].double().cpu().numpy()
+    S = xn @ W.T  # exact products; float64 sums err by < 2^-40 of sum |x w|
+    P = np.abs(xn) @ np.abs(W).T
+    err = np.abs(A - S)
+    model = 49 * 2.0 ** -23 * P * (1 + 2.0 ** -30) + 1e-30
+    assert np.isfinite(A).all()
+    assert (err <= model).all(), float((err / model).max())
+    assert (err <= 2.0 ** -17 * np.outer(nx, nw)).all()
+    assert np.allclose(nx, np.sqrt((xn * xn).sum(1)), rtol=1e-6, atol=0)
+    assert np.allclose(nw, np.sqrt((W * W).sum(1)), rtol=1e-6, atol=0)
+    with capsys.disabled():
+        print(f'\n[router bound, {mode}] max |A - S| / (49 2^-23 sum|x w|) = '
+              f'{float((err / model).max()):.3e}')
+
+
 @pytest.mark.parametrize('fmt', [0, 1])
 def test_tile_rows_layout(dev, fmt):
     """lm_w8_tile_rows against the index formula of its declaration, on a
