@@ -750,18 +750,19 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, c
 }
 
 // Approximate router logits of the prefill tokens: bf16 MFMA with fp32
-// accumulation (neither rounded to bf16 nor biased).  A workgroup owns 32
-// tokens x 64 experts; its four waves each take one quarter of K for the
-// whole tile (2 x 4 MFMA tiles, so every fragment read feeds two or four
-// MFMAs) and the quarters are summed through LDS at the end.  K is streamed
+// sums (neither rounded to bf16 nor biased).  A workgroup owns 32 tokens x
+// 64 experts; its four waves each take one quarter of K for the whole tile
+// (2 x 4 MFMA tiles, so every fragment read feeds two or four MFMAs) and the
+// quarters are summed through LDS at the end.  K is streamed
 // in 128-wide segments with coalesced loads: a wave load covers 4 whole
 // 256-byte row segments, one row per quarter-wave (a load in the MFMA
 // operand layout would touch 16 rows 4 KB apart per quarter-wave and keep
 // the address path stalled).  The segments go through the wave's own LDS
 // region (pitch 272 B, so the 16 rows of a fragment read fall in distinct
 // banks) and are read back in the MFMA layout; the next segment's loads are
-// in flight meanwhile.  The summation order does not matter:
-// prefill_topk_count_kernel bounds the error of any order.
+// in flight meanwhile.  Every MFMA sums its 32 products from zero and its
+// result is added to the wave's fp32 sum; prefill_topk_count_kernel's error
+// bound counts the roundings of exactly this scheme (31 + 15 + 3).
 constexpr int kRaTok = 32, kRaExp = 64;
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void
 router_approx_kernel(uint16_t *p_xn, const uint16_t *p_router_w, float *p_logits, int T, LayerArgs a) {
