@@ -885,12 +885,7 @@ __device__ void topk_exact_wave(const LayerArgs &a, int tok, int lane, unsigned 
                                 float *lv, int *cand, int *amb, int64_t *ids_out,
                                 uint16_t *w_out) {
   using T = typename KT::T;
-  u32x4 xv[4];  // the token's row, needed once the candidates are known
-  {
-    const uint16_t *xr = a.xn + (int64_t)tok * kH + lane * 8;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) xv[i] = ldg16(xr + 512 * i);
-  }
+  u32x4 xv[4];  // the token's row, loaded only when a candidate is open
   const float4 av = *reinterpret_cast<const float4 *>(a.logits + (int64_t)tok * kE + lane * 4);
   const float4 nv = *reinterpret_cast<const float4 *>(a.nw + lane * 4);
   const float nx = a.nx[tok];
@@ -977,7 +972,12 @@ __device__ void topk_exact_wave(const LayerArgs &a, int tok, int lane, unsigned 
       }
     }
   };
-  if (na > 0) fetch(0, 0);
+  if (na > 0) {
+    const uint16_t *xr = a.xn + (int64_t)tok * kH + lane * 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xv[i] = ldg16(xr + 512 * i);
+    fetch(0, 0);
+  }
   for (int c0 = 0; c0 < na; c0 += 2 * CB) {
     if (c0 + CB < na) fetch(1, c0 + CB);
     reduce(0, c0);
