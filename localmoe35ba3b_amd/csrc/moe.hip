@@ -665,28 +665,31 @@ __device__ __forceinline__ void router_row_norm(u32x4 wv, float *nw_out, float *
 // shared-gate logit gl (fp64 dot) and, when a.xh is set, the fp16 copy of the
 // row for the gate_up GEMM on fp16 tiles with its power of two xk.
 __device__ __forceinline__ void prefill_norm_token(u32x4 raw, const NormW &nwv, u32x4 gv,
-                                                   const LayerArgs &a, int tok, float *xf,
-                                                   float *red, float *red2, double *dred) {
+                                                   const LayerArgs &a, int tok, float *red,
+                                                   float *red2, double *dred) {
   const int t = threadIdx.x;
   constexpr int PER = kH / 256;
-  norm_row_to_lds(raw, nwv, a.eps, xf, red);
+  // the normalized values stay in the thread's registers: every use below
+  // reads the thread's own values (no LDS copy, no barrier for it)
+  float y[PER];
+  norm_row(raw, nwv, a.eps, red, y);
   {
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) ss += xf[t * PER + j] * xf[t * PER + j];
+    for (int j = 0; j < PER; ++j) ss += y[j] * y[j];
     ss = wave_sum_f32(ss);
     if ((t & 63) == 0) red2[t >> 6] = ss;
   }
   u32x4 packed;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    packed[j] = BF16::pack2(xf[t * PER + 2 * j], xf[t * PER + 2 * j + 1]);
+    packed[j] = BF16::pack2(y[2 * j], y[2 * j + 1]);
   *reinterpret_cast<u32x4 *>(a.xn + (int64_t)tok * kH + t * PER) = packed;
   double acc = 0.0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    acc = __builtin_fma((double)xf[t * PER + 2 * j], (double)bf16_bits_to_f32(gv[j] & 0xFFFFu), acc);
-    acc = __builtin_fma((double)xf[t * PER + 2 * j + 1], (double)bf16_bits_to_f32(gv[j] >> 16), acc);
+    acc = __builtin_fma((double)y[2 * j], (double)bf16_bits_to_f32(gv[j] & 0xFFFFu), acc);
+    acc = __builtin_fma((double)y[2 * j + 1], (double)bf16_bits_to_f32(gv[j] >> 16), acc);
   }
   acc = wave_sum_f64_dpp(acc);
   if ((t & 63) == 0) dred[t >> 6] = acc;
@@ -709,8 +712,8 @@ __device__ __forceinline__ void prefill_norm_token(u32x4 raw, const NormW &nwv, 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       f16x2 v;
-      v.x = (_Float16)ldexpf(xf[t * PER + 2 * j], k);
-      v.y = (_Float16)ldexpf(xf[t * PER + 2 * j + 1], k);
+      v.x = (_Float16)ldexpf(y[2 * j], k);
+      v.y = (_Float16)ldexpf(y[2 * j + 1], k);
       hp[j] = __builtin_bit_cast(uint32_t, v);
     }
     *reinterpret_cast<u32x4 *>(a.xh + (int64_t)tok * kH + t * PER) = hp;
@@ -726,7 +729,6 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, c
   a.router_w = p_router_w;
   a.gate_w = p_gate_w;
   a.norm_w = p_norm_w;
-  __shared__ float xf[kH];
   __shared__ float red[4];
   __shared__ float red2[4];
   __shared__ double dred[4];
@@ -744,8 +746,7 @@ __global__ __launch_bounds__(256) void prefill_norm_gate_kernel(uint16_t *p_h, c
     if (tok < kE) router_row_norm(wv, a.nw + tok, red2);
     return;
   }
-  prefill_norm_token(ldg16(a.h + (int64_t)tok * kH + t * PER), nwv, gv, a, tok, xf, red, red2,
-                     dred);
+  prefill_norm_token(ldg16(a.h + (int64_t)tok * kH + t * PER), nwv, gv, a, tok, red, red2, dred);
   if (tok < kE) router_row_norm(wv, a.nw + tok, red2);
 }
 
@@ -1241,7 +1242,6 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(int64_t *p_ids, co
   a.wts = p_wts;
   const int tok = blockIdx.x;
   const int c = threadIdx.x * 8;
-  __shared__ float xf[NEXT ? kH : 1];
   __shared__ float red[4], red2[4];
   __shared__ double dred[4];
   // the next layer's weights, requested first (their latency overlaps the combine)
@@ -1312,7 +1312,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(int64_t *p_ids, co
     b.norm_w = nx.norm_w;
     b.gate_w = nx.gate_w;
     b.xh = nx.xh;
-    prefill_norm_token(outv, nwv, gv, b, tok, xf, red, red2, dred);
+    prefill_norm_token(outv, nwv, gv, b, tok, red, red2, dred);
     if (tok < kE) router_row_norm(wv, a.nw + tok, red2);
   }
 }
