@@ -1109,7 +1109,7 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
   constexpr int Q = 16;  // row phases: wave q sums rows q, q + Q, ...
   static_assert(kE == 4 * 64, "a lane sums 4 experts' byte counts");
   __shared__ int ptot[Q][kE], ppre[Q][kE], bpre[kScanGroups][kE];
-  __shared__ int offs[kE + 1], toffs[kE], scratch[4];
+  __shared__ int offs[kE + 1], toffs[kE], scratch[4], tscratch[4];
   const int t = threadIdx.x;
   const int R = T * kTopK;
   const int r = blockIdx.x * kScanRoutes + t;
@@ -1152,29 +1152,39 @@ __global__ __launch_bounds__(1024) void prefill_scan_kernel(const int64_t *__res
       p += (j0 + j < nb) ? cj[j] : 0;
     }
   }
-  auto scan = [&](int v, int *total) {
-    const int ln = t & 63, wave = t >> 6;
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int u = __shfl_up(incl, o, 64);
-      if (ln >= o) incl += u;
-    }
-    if (ln == 63 && wave < 4) scratch[wave] = incl;
-    __syncthreads();
-    int base = 0;
-    for (int i = 0; i < wave && i < 4; ++i) base += scratch[i];
-    *total = scratch[0] + scratch[1] + scratch[2] + scratch[3];
-    __syncthreads();
-    return base + incl - v;
-  };
-  int all = 0;
-  const int ex = scan(c, &all);
+  // Exclusive prefix sums over the kE experts (threads 0 .. kE - 1, the
+  // first four waves) of the route counts c and the tile counts nt, in one
+  // pass: wave-level shuffle scans, then the four wave totals through LDS.
   // tiles: the shared expert's nst first, then expert e's nt at nst + tex
   const int nst = (T + kBM - 1) / kBM;
   const int nt = t < kE ? (c + kBM - 1) / kBM : 0;
-  int ntot = 0;
-  const int tex = scan(nt, &ntot);
+  int ex, tex, all, ntot;
+  {
+    const int ln = t & 63, wave = t >> 6;
+    int incl = c, tincl = nt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o, 64), tu = __shfl_up(tincl, o, 64);
+      if (ln >= o) {
+        incl += u;
+        tincl += tu;
+      }
+    }
+    if (ln == 63 && wave < 4) {
+      scratch[wave] = incl;
+      tscratch[wave] = tincl;
+    }
+    __syncthreads();
+    int base = 0, tbase = 0;
+    for (int i = 0; i < wave && i < 4; ++i) {
+      base += scratch[i];
+      tbase += tscratch[i];
+    }
+    all = scratch[0] + scratch[1] + scratch[2] + scratch[3];
+    ntot = tscratch[0] + tscratch[1] + tscratch[2] + tscratch[3];
+    ex = base + incl - c;
+    tex = tbase + tincl - nt;
+  }
   if (t < kE) {
     offs[t] = ex;
     toffs[t] = tex;
