@@ -132,10 +132,19 @@ __global__ __launch_bounds__(TH) void w8a8_gemv_kernel(GemvArgs a) {
   // would read every activation row from LDS once per weight piece.
   constexpr bool MF = MT >= 4 && KC != 0 && TH == 1024;
   static_assert(!MF || (32768 / KC) * (KC / 128) == 16 * (TH / 64), "one MFMA task per wave");
+  // With K fixed, QuantRows stages the rows: one 128-group per slot of LPG
+  // lanes (8 lanes from 8 rows, 16 from 4, a half-wave below), each slot a
+  // fixed group of every QSTEP-th row, QJ2 rows per slot.
+  constexpr int QG = KC ? KC / 128 : 1;
+  constexpr int LPG = MT >= 8 ? 8 : MT >= 4 ? 16 : 32;
+  constexpr bool QFIX = KC != 0 && (TH / LPG) % QG == 0;
+  constexpr int QSTEP = TH / LPG / QG > 0 ? TH / LPG / QG : 1;
+  constexpr int QJ2 = (MT + QSTEP - 1) / QSTEP;
+  using QS = typename std::conditional<QFIX, QuantRows<T, QJ2, QG, TH, LPG>, QuantStage<T, QJ>>::type;
   const int th = threadIdx.x;
   if (rv.rvalid * G <= LD * 8 * (TH / 64) && M * G <= TH &&
-      (QUANT ? M * G <= QJ * (TH / 32) : M * K <= XN * 16 * TH)) {
-    QuantStage<T, QJ> qst;
+      (QUANT ? (QFIX || M * G <= QJ * (TH / 32)) : M * K <= XN * 16 * TH)) {
+    QS qst;
     RowStage<XN> cst;
     if constexpr (QUANT)
       qst.load(a.x + (int64_t)rv.xrow * a.ldx, a.ldx, M, K);

@@ -228,6 +228,98 @@ struct QuantStage {
   }
 };
 
+// Absmax over aligned runs of LPG lanes (8, 16 or 32): the DPP steps of
+// halfwave_max that stay inside such a run.
+template <int LPG>
+__device__ __forceinline__ float group_max(float a) {
+  static_assert(LPG == 8 || LPG == 16 || LPG == 32, "lanes per group");
+  if constexpr (LPG == 32) {
+    return halfwave_max(a);
+  } else {
+    a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0xB1, 0xF, 0xF, false)));
+    a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x4E, 0xF, 0xF, false)));
+    a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x141, 0xF, 0xF, false)));
+    if constexpr (LPG == 16)
+      a = fmaxf(a, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x140, 0xF, 0xF, false)));
+    return a;
+  }
+}
+
+// QuantStage for a compile-time geometry: K = 128 G, TH threads, and LPG
+// lanes per 128-group (VPL = 128 / LPG values per lane, loaded as 8-byte
+// pieces like QuantStage's).  Group slot t (lanes LPG t ..) always takes
+// group t % G, of rows t / G + (TH / LPG / G) u, u < J, so the group offset
+// is fixed and each job adds one row stride: the generic stage's per-job
+// index division and 64-bit row products are gone.  Fewer lanes per group
+// give each lane more values, which spreads the per-group work (absmax,
+// scale, reciprocal) over fewer lanes' instructions: with 8 rows of 2048 a
+// 1024-thread block quantizes every group in one pass of 8-lane slots
+// instead of four passes of half-waves.  Rows past `rows` redo the last row
+// (the same bytes as its owner stores; no store is under a branch).  The
+// arithmetic per value is quantize_group's (w8a8.py:8-14), so the bytes and
+// scales are identical.  Covers up to J * TH / LPG / G rows.
+template <typename T, int J, int G, int TH, int LPG>
+struct QuantRows {
+  static constexpr int VPL = 128 / LPG, NSLOT = TH / LPG, STEP = NSLOT / G;
+  static_assert(NSLOT % G == 0 && VPL % 4 == 0, "whole rows per sweep of the group slots");
+  uint2 raw[J][VPL / 4];
+  int rows;
+  __device__ __forceinline__ void load(const uint16_t *x, int64_t ldx, int nrows, int) {
+    rows = nrows;
+    const int t = threadIdx.x / LPG, l = threadIdx.x % LPG;
+    const uint16_t *base = x + (t % G) * 128 + l * VPL;
+    const int m0 = t / G;
+#pragma unroll
+    for (int u = 0; u < J; ++u) {
+      const uint16_t *p = base + (int64_t)min(m0 + STEP * u, rows - 1) * ldx;
+#pragma unroll
+      for (int i = 0; i < VPL / 4; ++i) raw[u][i] = ldg_u2(p + 4 * i);
+    }
+  }
+  __device__ __forceinline__ void store(int, int8_t *xq, float *xs) const {
+    const int t = threadIdx.x / LPG, l = threadIdx.x % LPG;
+    const int g = t % G, m0 = t / G;
+    const float inv127 = (float)(1.0 / 127.0);
+#pragma unroll
+    for (int u = 0; u < J; ++u) {
+      const int m = min(m0 + STEP * u, rows - 1);
+      float v[VPL];
+#pragma unroll
+      for (int i = 0; i < VPL / 4; ++i) {
+        v[4 * i] = T::to_f32(raw[u][i].x & 0xFFFFu);
+        v[4 * i + 1] = T::to_f32(raw[u][i].x >> 16);
+        v[4 * i + 2] = T::to_f32(raw[u][i].y & 0xFFFFu);
+        v[4 * i + 3] = T::to_f32(raw[u][i].y >> 16);
+      }
+      float a = 0.0f;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) a = fmaxf(a, fabsf(v[i]));
+      a = group_max<LPG>(a);
+      const float sc = fmaxf(a, 1e-10f) * inv127;
+      const float r = 1.0f / sc;
+      uint32_t packed[VPL / 4];
+#pragma unroll
+      for (int i = 0; i < VPL / 4; ++i) {
+        packed[i] = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          packed[i] |= ((uint32_t)(uint8_t)(int8_t)(int)rintf(quant_div(v[4 * i + k], sc, r)))
+                       << (8 * k);
+      }
+      int8_t *dst = xq + m * (G * 128) + g * 128 + l * VPL;
+      if constexpr (VPL == 4) {
+        *reinterpret_cast<uint32_t *>(dst) = packed[0];
+      } else if constexpr (VPL == 8) {
+        *reinterpret_cast<uint2 *>(dst) = uint2{packed[0], packed[1]};
+      } else {
+        static_assert(VPL == 16, "values per lane");
+        *reinterpret_cast<u32x4 *>(dst) = u32x4{packed[0], packed[1], packed[2], packed[3]};
+      }
+      if (l == 0) xs[m * G + g] = sc;
+    }
+  }
+};
+
 // Per-row dynamic quantization of `rows` activation rows of K 16-bit values
 // into LDS (w8a8.py:8-14).  Each 128-group is handled by 32 lanes.
 template <typename T>
