@@ -964,22 +964,29 @@ constexpr int kGroupedBN = 128;  // grouped_mfma_kernel tile columns
 constexpr int kRbBMTall = 128;
 constexpr int kRbADTall = 3;
 constexpr int64_t kDenseTallM = 1024;
+// Wide dense tiles: 8 waves over 256 columns of a 128-row tile, one
+// workgroup per CU.  Each activation stage then feeds twice the columns, a
+// third fewer wave-loads per MFMA than two 4-wave workgroups; taken when the
+// launch still gives each of the 256 CUs a tile.
+constexpr int kRbNWWide = 8;
+constexpr int64_t kRbWideTiles = 256;
 
-template <typename T, bool SWIGLU, bool GATHER, int WL, int K, int BM = 96>
+template <typename T, bool SWIGLU, bool GATHER, int WL, int K, int BM = 96, int NW = kRbNW>
 static int launch_rb(GemmArgs a, unsigned mtiles, hipStream_t st) {
   constexpr bool TILES = WL == kWlTiles || WL == kWlTilesF16;
   constexpr bool TALL = BM == kRbBMTall;
   static_assert(!TALL || (WL == kWlDirect && !SWIGLU && !GATHER), "tall tiles serve dense rows");
+  static_assert(NW == kRbNW || (TALL && NW == kRbNWWide), "wide tiles serve dense tall rows");
   constexpr int TN = TILES ? kRbTnTiles : kRbTN;
-  constexpr int OCC = TILES || TALL ? kRbOccTiles : kRbOcc;
+  constexpr int OCC = NW == kRbNWWide ? 1 : TILES || TALL ? kRbOccTiles : kRbOcc;
   constexpr int AD = TALL ? kRbADTall : kRbAD;
-  constexpr int RBN = kRbNW * TN;
+  constexpr int RBN = NW * TN;
   a.nt_count = SWIGLU ? (int)cdiv(a.N / 2, RBN / 2) : (int)cdiv(a.N, RBN);
   a.mt_count = (int)mtiles;
   const int64_t grid = xcd_grid(a.mt_count, a.nt_count);
   LM_REQUIRE(grid < (int64_t(1) << 31), LM_EINVAL, "problem too large for one launch");
-  grouped_rb_kernel<T, SWIGLU, GATHER, WL, K, BM, TN, kRbBD, kRbHL, AD, kRbNW, OCC>
-      <<<(unsigned)grid, kRbNW * 64, 0, st>>>(a);
+  grouped_rb_kernel<T, SWIGLU, GATHER, WL, K, BM, TN, kRbBD, kRbHL, AD, NW, OCC>
+      <<<(unsigned)grid, NW * 64, 0, st>>>(a);
   return check_launch("grouped_rb_kernel");
 }
 
@@ -989,9 +996,14 @@ template <typename T, bool SWIGLU, bool GATHER, int WL>
 static int launch_grouped(GemmArgs a, unsigned mtiles, hipStream_t st) {
   if (mtiles == 0) return LM_OK;
   if constexpr (WL == kWlDirect && !SWIGLU && !GATHER) {
-    if (!a.table && a.tile_rows == kRbBMTall && (a.K == 2048 || a.K == 512))
+    if (!a.table && a.tile_rows == kRbBMTall && (a.K == 2048 || a.K == 512)) {
+      if ((int64_t)mtiles * cdiv(a.N, kRbNWWide * kRbTN) >= kRbWideTiles)
+        return a.K == 2048
+                   ? launch_rb<T, false, false, WL, 2048, kRbBMTall, kRbNWWide>(a, mtiles, st)
+                   : launch_rb<T, false, false, WL, 512, kRbBMTall, kRbNWWide>(a, mtiles, st);
       return a.K == 2048 ? launch_rb<T, false, false, WL, 2048, kRbBMTall>(a, mtiles, st)
                          : launch_rb<T, false, false, WL, 512, kRbBMTall>(a, mtiles, st);
+    }
   }
   if (a.tile_rows <= 96 && (a.K == 2048 || a.K == 512))
     return a.K == 2048 ? launch_rb<T, SWIGLU, GATHER, WL, 2048>(a, mtiles, st)
