@@ -154,11 +154,15 @@ def test_w8a8_grouped_decode_bit_exact(dev):
 # ------------------------------------------------------------- a2 W8A16
 @pytest.mark.parametrize('m,n,k', [(1, 4096, 2048), (2048, 4096, 2048), (3, 1000, 384),
                                    (37, 1000, 384), (8, 512, 2048), (130, 2048, 512),
-                                   (1057, 4096, 2048), (1100, 1000, 512)])
+                                   (1057, 4096, 2048), (1100, 1000, 512), (3000, 3000, 2048),
+                                   (4096, 2048, 512)])
 def test_w8a16_linear(dev, m, n, k):
     """Every GEMM path of int8.linear against the oracle: the GEMV (m <= 8),
     96-row tiles, 128-row tiles from m = 1024 (1057 and 1100 end in partial
-    tiles of 33 and 76 rows), the generic kernel at K = 384."""
+    tiles of 33 and 76 rows), the wide 8-wave 256-column tiles where they give
+    every CU a tile (2048 x 4096, 3000 x 3000 with a partial row tile of 56
+    rows and a partial column tile of 184 columns, and K = 512), the generic
+    kernel at K = 384."""
     gen = seeded(m + n)
     x = bf16_rand((m, k), gen)
     wq, ws = O.quantize_weight((torch.randn(n, k, generator=gen) * 0.02).numpy())
@@ -166,14 +170,15 @@ def test_w8a16_linear(dev, m, n, k):
     assert_close(npf(y), O.w8a16_linear(npf(x), wq, ws), BF16_TOL, f'w8a16 {m}x{n}x{k}')
 
 
-@pytest.mark.parametrize('m', [1, 5, 300, 1030])
-def test_w8a16_linear_exact(dev, m):
+@pytest.mark.parametrize('m,n', [(1, 384), (5, 384), (300, 384), (1030, 384), (4000, 2048)])
+def test_w8a16_linear_exact(dev, m, n):
     """Integer activations and power-of-two scales make every product and sum
-    exact in fp32, so any MFMA/GEMV layout or dequant error shows bit for bit."""
+    exact in fp32, so any MFMA/GEMV layout or dequant error shows bit for bit
+    (4000 x 2048 runs the wide 8-wave tiles, ending in a 32-row tile)."""
     g = np.random.default_rng(m)
     x = g.integers(-8, 9, size=(m, 512)).astype(np.float32)
-    q = g.integers(-127, 128, size=(384, 512)).astype(np.int8)
-    s = np.full((384, 4), 2.0 ** -6, np.float32)
+    q = g.integers(-127, 128, size=(n, 512)).astype(np.int8)
+    s = np.full((n, 4), 2.0 ** -6, np.float32)
     s[::3] = 2.0 ** -5
     y = int8.linear(torch.from_numpy(x).to(torch.bfloat16).to(dev), torch.from_numpy(q).to(dev),
                     torch.from_numpy(s).to(dev))
