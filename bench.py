@@ -183,7 +183,9 @@ def isolated_probe(dev, spin_cycles, reps=32):
     decode layer, timed per kernel in the request).  The GEMVs also report
     `graph_us`, the per-launch time of 64 launches replayed as one HIP graph,
     and `launch_floor` gives both timings of a one-element fill: per-launch
-    events cost about as much as a short kernel itself."""
+    events cost about as much as a short kernel itself.
+    `w8a8_gate_up_swiglu_m8_over_m1` is the 8-row time over the one-row time,
+    in both timings."""
     from localmoe35ba3b_amd.convert import quantize_g128
     from localmoe35ba3b_amd.operators import int8, w8a8
     gen = torch.Generator(device=dev)
@@ -273,6 +275,9 @@ def isolated_probe(dev, spin_cycles, reps=32):
         out[f'w8a8_gate_up_swiglu_m{m}'] = hbm(
             run(fnm, reps), GU_EXPERT_BYTES + H * 2 * m + I * 2 * m,
             f'[{m}, 2048] x [1024, 2048] int8 g128', run_graph(fnm, 64))
+    m1, m8 = out['w8a8_gate_up_swiglu_m1'], out['w8a8_gate_up_swiglu_m8']
+    out['w8a8_gate_up_swiglu_m8_over_m1'] = {'event': round(m8['avg_us'] / m1['avg_us'], 3),
+                                             'graph': round(m8['graph_us'] / m1['graph_us'], 3)}
     return out
 
 
