@@ -51,6 +51,10 @@ def parse():
     p.add_argument('--copy-probe', action='store_true',
                    help='only run a plain streaming kernel over 256 MiB (torch.neg on int32, '
                         'five launches): the known-size reference for HBM traffic counters')
+    p.add_argument('--power-probe', action='store_true',
+                   help='only replay the two-chunk prefill graph back to back for about 6 s while '
+                        'sampling the board power and graphics clocks with amd-smi; also time '
+                        'replays that follow a 30 ms idle gap')
     return p.parse_args()
 
 
@@ -63,6 +67,92 @@ def copy_probe(dev):
     torch.cuda.synchronize()
     print(json.dumps({'copy_probe': 'torch.neg int32', 'bytes_read_per_launch': n * 4,
                       'bytes_written_per_launch': n * 4, 'launches': 5}), flush=True)
+
+
+def power_probe(stack, dev, seconds=6.0):
+    """Board power and graphics clocks while the two-chunk prefill graph
+    replays back to back (amd-smi sampled from a host thread), and the replay
+    time back to back against after a 30 ms idle gap.  Prints one JSON line."""
+    import subprocess
+    import threading
+    x = torch.randn((PREFILL_TOKENS, H), device=dev).to(torch.bfloat16)
+    pst = x.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        stack.prefill_(pst.clone(), CHUNK)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        stack.prefill_(pst, CHUNK)
+    torch.cuda.synchronize()
+    samples, phase, stop = [], ['idle'], [False]
+
+    def sample():
+        while not stop[0]:
+            try:
+                out = subprocess.run(['amd-smi', 'metric', '-g', '0', '-p', '-c', '--json'],
+                                     capture_output=True, text=True, timeout=5).stdout
+                d = json.loads(out)
+                d = d['gpu_data'][0] if isinstance(d, dict) and 'gpu_data' in d else d[0]
+                clk = d['clock']
+                gfx = [v['clk']['value'] for k, v in clk.items() if k.startswith('gfx_')
+                       and isinstance(v, dict) and isinstance(v.get('clk'), dict)
+                       and isinstance(v['clk'].get('value'), (int, float))]
+                pw = d['power']['socket_power']
+                samples.append((phase[0], min(gfx), max(gfx),
+                                pw['value'] if isinstance(pw, dict) else pw))
+            except Exception as e:  # no amd-smi, or another output format
+                samples.append((phase[0], None, None, repr(e)[:80]))
+            time.sleep(0.05)
+
+    th = threading.Thread(target=sample)
+    th.start()
+    time.sleep(1.0)
+    phase[0] = 'prefill'
+    ev = []
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            a, b = make_events(2)
+            a.record()
+            pst.copy_(x)
+            graph.replay()
+            b.record()
+            ev.append((a, b))
+        torch.cuda.synchronize()
+    phase[0] = 'after'
+    time.sleep(1.0)
+    stop[0] = True
+    th.join()
+    back_to_back = sorted(a.elapsed_time(b) for a, b in ev)
+    gapped = []
+    for _ in range(10):
+        time.sleep(0.03)
+        a, b = make_events(2)
+        a.record()
+        pst.copy_(x)
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        gapped.append(a.elapsed_time(b))
+    gapped.sort()
+
+    def stats(tag):
+        rows = [r for r in samples if r[0] == tag and r[1] is not None]
+        if not rows:
+            return None
+        pw = sorted(r[3] for r in rows)
+        lo = sorted(r[1] for r in rows)  # per sample, the slowest of the XCDs' clocks
+        return {'samples': len(rows), 'gfx_mhz_min': lo[0], 'gfx_mhz_median': lo[len(lo) // 2],
+                'gfx_mhz_max': max(r[2] for r in rows), 'socket_w_median': pw[len(pw) // 2],
+                'socket_w_max': pw[-1]}
+    print(json.dumps({'power_probe': 'two-chunk prefill graph replayed back to back',
+                      'replays': len(ev),
+                      'replay_ms_median': round(back_to_back[len(back_to_back) // 2], 3),
+                      'replay_ms_after_30ms_idle_median': round(gapped[len(gapped) // 2], 3),
+                      'idle': stats('idle'), 'prefill': stats('prefill'),
+                      'errors': sorted({r[3] for r in samples if r[1] is None})[:3]}), flush=True)
 
 
 def log(msg):
@@ -448,6 +538,9 @@ def main():
     t_build = time.perf_counter()
     stack = SyntheticMoEStack(layers=args.layers, seed=4, device=dev, max_tokens=CHUNK)
     torch.cuda.synchronize()
+    if args.power_probe:
+        power_probe(stack, dev)
+        return
     t_build = time.perf_counter() - t_build
     log(f'stack built: {stack.L} layers, {stack.bank_bytes() / 1e9:.2f} GB in HBM, {t_build:.1f} s')
     gen = torch.Generator(device=dev)
