@@ -71,8 +71,9 @@ def copy_probe(dev):
 
 def power_probe(stack, dev, seconds=6.0):
     """Board power and graphics clocks while the two-chunk prefill graph
-    replays back to back (amd-smi sampled from a host thread), and the replay
-    time back to back against after a 30 ms idle gap.  Prints one JSON line."""
+    replays back to back, then while the 40-layer decode step does (amd-smi
+    sampled from a host thread), and the prefill replay time back to back
+    against after a 30 ms idle gap.  Prints one JSON line."""
     import subprocess
     import threading
     x = torch.randn((PREFILL_TOKENS, H), device=dev).to(torch.bfloat16)
@@ -121,6 +122,23 @@ def power_probe(stack, dev, seconds=6.0):
             b.record()
             ev.append((a, b))
         torch.cuda.synchronize()
+    # the 40-layer decode step, replayed back to back for comparison
+    tok = torch.randn((1, H), device=dev).to(torch.bfloat16)
+    dst = tok.clone()
+    with torch.cuda.stream(side):
+        stack.forward(dst.clone())
+    torch.cuda.current_stream().wait_stream(side)
+    dgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(dgraph):
+        stack.forward(dst)
+    torch.cuda.synchronize()
+    phase[0] = 'decode'
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds / 2:
+        for _ in range(100):
+            dst.copy_(tok)
+            dgraph.replay()
+        torch.cuda.synchronize()
     phase[0] = 'after'
     time.sleep(1.0)
     stop[0] = True
@@ -151,7 +169,7 @@ def power_probe(stack, dev, seconds=6.0):
                       'replays': len(ev),
                       'replay_ms_median': round(back_to_back[len(back_to_back) // 2], 3),
                       'replay_ms_after_30ms_idle_median': round(gapped[len(gapped) // 2], 3),
-                      'idle': stats('idle'), 'prefill': stats('prefill'),
+                      'idle': stats('idle'), 'prefill': stats('prefill'), 'decode': stats('decode'),
                       'errors': sorted({r[3] for r in samples if r[1] is None})[:3]}), flush=True)
 
 
