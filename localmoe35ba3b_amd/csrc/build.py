@@ -31,7 +31,9 @@ COMMON = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}', '-ffp-contract
 # The VGPR form of the MFMA instructions: the prefill router adds each MFMA
 # result to an fp32 sum on the VALU, which reads VGPR results directly
 # instead of copying them out of AGPRs (the router is moe.hip's only MFMA
-# user).
+# user).  gemm.hip keeps the default flags: its register-streamed GEMMs
+# already hold their accumulators in VGPRs, and the same two flags there
+# left the prefill unchanged.
 EXTRA = {'moe.hip': ['-mllvm', '-amdgpu-kernarg-preload-count=6',
                      '-mllvm', '-amdgpu-mfma-vgpr-form=1']}
 
